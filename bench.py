@@ -1,0 +1,159 @@
+"""Benchmark: pi0.5 flow-matching denoise loop on one MI355X.
+
+One "step" = one full action chunk: the 10-step Euler loop of the 18-layer pi0.5 expert over a
+968-token prefix KV cache for 50 action tokens, bf16 operands / fp32 accumulation, batch 1,
+as ONE cooperative kernel launch. Inputs are seeded synthetic tensors already resident in HBM.
+
+Prints one JSON line: value = ms per chunk (lower is better), the roofline of the kernel
+(algorithmic bytes / measured launch time vs 8 TB/s), the CPU fp32 oracle timed on the host
+cores (cpu_baseline), and the parity of the first GPU chunk vs that oracle run.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from flashact_amd import pi05, synthetic  # noqa: E402
+
+NL, D, HD, F, AD = 18, 1024, 256, 4096, 32
+LP, TV, S = 968, 50, 10
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes_per_chunk(nl=NL, lp=LP, tv=TV, s=S) -> int:
+    """HBM bytes one chunk must move: bf16 expert weights + prefix K/V + suffix K/V + fp32 mods
+    + fp32 action in/out projections, per Euler step, times the number of steps."""
+    params_per_layer = (2560 * D) + (D * 2048) + (8192 * D) + (D * F)
+    weights = nl * params_per_layer * 2
+    prefix_kv = nl * lp * HD * 2 * 2
+    suffix_kv = nl * tv * HD * 2 * 2
+    mods = (2 * nl + 1) * 3 * D * 4
+    action_io = (D * AD + D + AD * D + AD) * 4
+    return s * (weights + prefix_kv + suffix_kv + mods + action_io)
+
+
+def build_inputs(dev, seed=0):
+    w = synthetic.pi05_weights(seed, dev, NL=NL)
+    inp = synthetic.pi05_inputs(seed + 1, dev, batch=1, NL=NL, Lp=LP, Tv=TV)
+    mods, modf = pi05.precompute_mods(S, w["w_ti"], w["b_ti"], w["w_to"], w["b_to"], w["w_in"], w["b_in"],
+                                      w["w_post"], w["b_post"], w["w_fin"], w["b_fin"])
+    for k in ("w_in", "w_post", "b_in", "b_post", "w_ti", "w_to", "b_ti", "b_to", "w_fin", "b_fin"):
+        del w[k]
+    packed = pi05.pack_weights(w["wq"], w["wk"], w["wv"], w["wo"], w["wg"], w["wu"], w["wd"])
+    cos, sin = pi05.rope_table(LP, TV, device=dev)
+    Lmax = pi05.lmax_for(LP, TV)
+    kv = torch.stack([inp["kpre"][0], inp["vpre"][0]], dim=1)
+    kc, vc = pi05.make_caches(kv, Lmax)
+    return w, inp, mods, modf, packed, cos, sin, Lmax, kc, vc
+
+
+def cpu_baseline(w, inp, mods, modf, cos, sin, steps=S):
+    """CPU fp32 oracle (OpenMP over the host cores) on the same inputs; returns (ms/chunk, x_t, threads)."""
+    from oracle import oracle as O
+
+    def u16(t):
+        return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+    ow = {k: u16(w[k]) for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")}
+    ow.update(mods=mods[:steps].cpu().numpy(), mod_final=modf[:steps].cpu().numpy(), rope_cos=cos.cpu().numpy(),
+              rope_sin=sin.cpu().numpy(), w_ain=w["w_ain"].cpu().numpy(), b_ain=w["b_ain"].cpu().numpy(),
+              w_aout=w["w_aout"].cpu().numpy(), b_aout=w["b_aout"].cpu().numpy(),
+              kpre=u16(inp["kpre"]), vpre=u16(inp["vpre"]))
+    x0 = inp["noise"].cpu().numpy()
+    t0 = time.perf_counter()
+    out = O.pi05_denoise(ow, x0, Lp=LP, Tv=TV, S=steps, NL=NL)
+    dt = time.perf_counter() - t0
+    return dt * 1000.0 * (S / steps), out, O.num_threads()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline and parity check")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the pi0.5/MolmoAct2 denoise loop is a single-GPU "
+                                   "kernel (batch-DP sharding needs no exchange; see DESIGN.md)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    w, inp, mods, modf, packed, cos, sin, Lmax, kc, vc = build_inputs(dev)
+    x_t = inp["noise"][0].clone()
+    empty = torch.empty(0, device=dev)
+
+    def step():
+        pi05.launch(packed["w1"], packed["wo"], packed["w2"], packed["w3"], empty, empty, empty, empty, mods, modf,
+                    cos, sin, w["w_ain"], w["b_ain"], w["w_aout"], w["b_aout"], None, None, 0, kc, vc, LP, Lmax,
+                    S, TV, x_t)
+
+    step()  # first chunk: compared against the CPU oracle below
+    torch.cuda.synchronize()
+    first = x_t.detach().cpu().numpy().copy()
+    status = pi05.read_status(pi05.workspace(dev))
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t_wall = time.perf_counter()
+    for e0, e1 in evs:
+        e0.record(stream)
+        step()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    per = np.array([e0.elapsed_time(e1) for e0, e1 in evs])
+    total_ms = evs[0][0].elapsed_time(evs[-1][1])
+    ms_per_step = total_ms / args.steps
+    status |= pi05.read_status(pi05.workspace(dev))
+
+    nbytes = algorithmic_bytes_per_chunk()
+    kern_ms = float(per.mean())
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    res = {
+        "metric": "ms per 50x32 action chunk (10 steps, bs=1) + % HBM roofline; chunks/s at bs=16",
+        "value": round(ms_per_step, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) bf16 weights, N(0,1) prefix KV and noise)",
+        "config": {"workload": "pi05_expert_bs1_T50_Lp968_S10", "layers": NL, "batch": 1, "action_tokens": TV,
+                   "prefix_len": LP, "euler_steps": S, "launches_per_chunk": 1},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": nbytes, "kernel_ms_mean": round(kern_ms, 4),
+                     "kernel_ms_p50": round(float(np.median(per)), 4), "kernel_ms_min": round(float(per.min()), 4)},
+        "wall_ms_per_step": round(t_wall * 1000.0 / args.steps, 4),
+        "kernel_status": status,
+    }
+    if not args.no_cpu:
+        cpu_ms, ref, threads = cpu_baseline(w, inp, mods, modf, cos, sin)
+        d = np.abs(first[:TV].astype(np.float64) - ref[0].astype(np.float64))
+        a, b = first[:TV].ravel().astype(np.float64), ref[0].ravel().astype(np.float64)
+        res["cpu_baseline"] = {"value": round(cpu_ms, 1), "unit": "ms per chunk", "cores": threads, "kind": "port",
+                               "sample": "one full chunk (18 layers x 10 Euler steps, Lp=968, Tv=50), fp32 oracle "
+                                         "oracle/fa_oracle.c, OpenMP"}
+        res["parity"] = {"max_abs": float(d.max()), "mean_abs": float(d.mean()),
+                         "cos": float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b))),
+                         "tolerance": {"max_abs": 2e-2, "mean_abs": 2e-3}}
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,159 @@
+// Device-side building blocks shared by the MI355X (gfx950) denoise kernels.
+//
+// Memory-coherence model used by every kernel in this library (measured on MI355X):
+//  * Each XCD (32 CUs) has a private L2. A CU's stores go write-through L1 -> its XCD's L2.
+//  * Data exchanged between CUs of the SAME XCD: plain stores, device-scope (sc1) loads.
+//    sc1 loads bypass L1 and see L2-resident data written by sibling CUs.
+//  * Data exchanged ACROSS XCDs: sc1 stores (write-through to memory) and sc1 loads.
+//  * Barriers are epoch flags, never RMW atomics: a workgroup publishes its epoch with one
+//    store; waiters poll a flag line with one sc1 vector load per lane.
+//      XCD barrier  : flag line in the XCD's L2 (~0.5 us).
+//      grid barrier : XCD barrier, then each XCD's rank-0 workgroup publishes the epoch with an
+//                     sc1 store to an 8-entry line that every workgroup polls.
+//    No agent-scope L2 writeback/invalidate (buffer_wbl2 / buffer_inv) is issued anywhere: on
+//    MI355X those cost ~4 us per barrier.
+//  * Every wait is capped; a cap hit sets a sticky error bit that makes all later waits return
+//    at once, so a broken launch always drains instead of hanging.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Cache-policy operand of gfx950 buffer instructions.
+constexpr int kCpPlain = 0;
+constexpr int kCpSc1 = 16;   // device scope: bypass L1, coherent across CUs/XCDs
+constexpr int kRsrcWord3 = 0x00020000;
+
+// Sticky error bits written into the workspace control block.
+constexpr unsigned kErrSpin = 1u;   // a barrier wait hit its cap
+constexpr unsigned kErrXcd = 2u;    // blockIdx -> XCD mapping differs from the assumed round robin
+constexpr unsigned kSpinCap = 1u << 20;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+
+template <int CP>
+__device__ __forceinline__ u32x4 ldb128(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP);
+}
+template <int CP>
+__device__ __forceinline__ u32x2 ldb64(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CP);
+}
+template <int CP>
+__device__ __forceinline__ float ldbf32(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CP));
+}
+template <int CP>
+__device__ __forceinline__ unsigned short ldb16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, CP);
+}
+template <int CP>
+__device__ __forceinline__ void stb128(rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, CP);
+}
+
+__device__ __forceinline__ u32x4 ld_stream128(const void* p) {  // weights: read once per step
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  // D[16x16] += A[16x32] * B[32x16]. Lane l: A row l%16, B col l%16, k = 8*(l/16)..+7;
+  // D rows 4*(l/16)+i, col l%16.
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+
+__device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
+__device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
+  bf16x2 v = {(bf16)a, (bf16)b};
+  return __builtin_bit_cast(unsigned, v);
+}
+__device__ __forceinline__ float bf_lo(unsigned u) { return __builtin_bit_cast(float, u << 16); }
+__device__ __forceinline__ float bf_hi(unsigned u) { return __builtin_bit_cast(float, u & 0xffff0000u); }
+
+__device__ __forceinline__ unsigned xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 7u; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // GeLU with the tanh approximation (Hendrycks & Gimpel 2016).
+  const float k0 = 0.7978845608028654f;
+  return 0.5f * x * (1.0f + tanhf(k0 * (x + 0.044715f * x * x * x)));
+}
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// ---------------------------------------------------------------- barriers
+struct Sync {
+  uint64_t* xline;  // this XCD's flag line, one slot per rank
+  uint64_t* gline;  // one slot per XCD
+  unsigned* err;
+  uint64_t e;       // epoch of the most recent arrive
+  int rank, xcd, nrank, nxcd;
+};
+
+__device__ __forceinline__ uint64_t ld_flag(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One full wave polls p[0..n) until every entry >= e.
+__device__ __forceinline__ void poll_wave(const uint64_t* p, int n, uint64_t e, unsigned* err) {
+  if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin) return;
+  const int lane = threadIdx.x & 63;
+  for (unsigned it = 0;; ++it) {
+    uint64_t v = lane < n ? ld_flag(p + lane) : ~0ull;
+    if (__all(v >= e)) return;
+    if (it > kSpinCap) {
+      if (lane == 0) atomicOr(err, kErrSpin);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Publish this workgroup's epoch. All of the workgroup's prior global stores are complete
+// (vmcnt drained) before the flag store issues.
+__device__ __forceinline__ void sync_arrive(Sync& s) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  s.e += 1;
+  if (threadIdx.x == 0) __hip_atomic_store(&s.xline[s.rank], s.e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void sync_wait_xcd(Sync& s) {
+  if (threadIdx.x < 64) poll_wave(s.xline, s.nrank, s.e, s.err);
+  __syncthreads();
+}
+
+__device__ __forceinline__ void sync_wait_grid(Sync& s) {
+  if (threadIdx.x < 64) {
+    if (s.rank == 0) {
+      poll_wave(s.xline, s.nrank, s.e, s.err);
+      if (threadIdx.x == 0) __hip_atomic_store(&s.gline[s.xcd], s.e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    poll_wave(s.gline, s.nxcd, s.e, s.err);
+  }
+  __syncthreads();
+}
+
+}  // namespace fa

@@ -1,0 +1,27 @@
+// Host-side helpers shared by the C-ABI launchers: thread-local error text and the
+// device / cooperative-capacity checks run before every launch.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace fa {
+namespace host {
+
+char* error_buffer();  // thread-local, 512 bytes (capi.hip)
+
+inline int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(error_buffer(), 512, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+// Verifies the current device is a 256-CU gfx950 with cooperative launch, raises the
+// kernel's dynamic-LDS limit (once per device and kernel) and checks that `nwg`
+// workgroups of `threads` threads can be co-resident.
+int check_device(const void* kernel, int threads, unsigned lds_bytes, int nwg, const char* who);
+
+}  // namespace host
+}  // namespace fa

@@ -1,0 +1,125 @@
+/*
+ * flashact_mi355x.h -- C ABI of the MI355X (gfx950) flow-matching denoise engine.
+ *
+ * Plain C: pointers, sizes and ints only. Every device pointer is HIP device memory owned
+ * by the caller; no entry point allocates, frees or synchronises. Work is enqueued on the
+ * given stream (a hipStream_t; NULL = the default stream). Entry points return FA_OK (0) or
+ * an FA_ERR_* code; fa_last_error() returns the message of the calling thread's last failure.
+ *
+ * Reference interfaces replaced (paths relative to the FlashAct source tree):
+ *   fa_pi05_denoise ....... `launch(...)` of the mk_v6 torch extension, src/pi05/binding.cpp:28-68
+ *                            (kernel pi05_megakernel, src/pi05/mk6.cu:112-519)
+ *   fa_ma2_flow ........... `launch(...)` of the mk_ma2 torch extension, src/molmoact2/binding.cpp:28-83
+ *                            (kernel ma2_megakernel, src/molmoact2/mk_ma2.cu:103-576)
+ *   fa_*_workspace_bytes,
+ *   fa_*_workspace_init ... the reference's caller-allocated scratch tensors
+ *                            (src/pi05/binding.cpp:34-36, src/molmoact2/binding.cpp:33-34)
+ *   fa_last_error ......... TORCH_CHECK on the launch status (src/pi05/binding.cpp:67)
+ *   fa_device_query ....... the occupancy clamp / diagnostics of src/molmoact2/binding.cpp:65-79
+ *   fa_abi_version ........ no counterpart (ABI guard for the Python and C++ callers)
+ */
+#ifndef FLASHACT_MI355X_H
+#define FLASHACT_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+struct ihipStream_t;
+typedef struct ihipStream_t* fa_stream_t; /* identical to hipStream_t */
+
+enum fa_status {
+  FA_OK = 0,
+  FA_ERR_INVALID_ARG = 1,  /* bad shape, null or misaligned pointer, workspace too small */
+  FA_ERR_UNSUPPORTED = 2,  /* valid request this build does not implement (e.g. fp8 weights) */
+  FA_ERR_DEVICE = 3,       /* not a 256-CU gfx950, or cooperative launch unavailable */
+  FA_ERR_LAUNCH = 4        /* the HIP launch itself failed */
+};
+
+enum fa_dtype { FA_DTYPE_BF16 = 0, FA_DTYPE_FP8_E4M3 = 1 };
+
+/* Kernel-side status bits (read back from the workspace by fa_*_read_status). */
+#define FA_KSTATUS_SPIN_TIMEOUT 1u /* a grid/XCD barrier wait hit its cap: results invalid */
+#define FA_KSTATUS_XCD_MAP 2u      /* workgroup -> XCD placement differed from round robin */
+
+typedef struct fa_device_info {
+  int cus;               /* compute units */
+  int xcds;              /* accelerator complex dies */
+  int lds_bytes;         /* LDS per workgroup */
+  int coop_launch;       /* cooperative launch supported */
+  int coop_max_blocks;   /* max co-resident workgroups of the pi0.5 kernel */
+  char arch[64];         /* gcnArchName */
+} fa_device_info;
+
+/* ---------------------------------------------------------------- pi0.5 expert
+ * D=1024, 8 query heads / 1 KV head, head_dim 256, F=4096, action dim 32.
+ * Weight packing is the reference's (src/pi05/hybrid_model.py:94-110):
+ *   w1 [NL][2560][1024]: rows 2p, 2p+1 = q rows (h*256+j, h*256+j+128), p = h*128+j;
+ *                        rows 2048+2j, 2048+2j+1 = k rows (j, j+128); rows 2304.. = v rows.
+ *   wo [NL][1024][2048]; w2 [NL][8192][1024]: rows 2f = gate f, 2f+1 = up f; w3 [NL][1024][4096].
+ * mods [S][NL][2][3072] (scale | shift | gate, for input/post-attention norms), mod_final [S][3072].
+ * rope_cos/sin [Tv][128] for positions Lp + t. w_ain [1024][32], b_ain [1024], w_aout [32][1024],
+ * b_aout [32] (fp32). kcache bf16 [batch][NL][Lmax][256] holds RoPE'd prefix keys in rows [0, Lp);
+ * vtcache bf16 [batch][NL][256][Lmax] holds the transposed prefix values in columns [0, Lp).
+ * The launch writes the suffix rows/columns [Lp, Lp+Tv) of both caches (as the reference does)
+ * and updates x_t in place: x_t [batch][xt_rows][32] fp32, rows [0, Tv) of each sample.
+ */
+typedef struct fa_pi05_args {
+  int weight_dtype; /* FA_DTYPE_BF16 (FA_DTYPE_FP8_E4M3 reserved) */
+  const void* w1;
+  const void* wo;
+  const void* w2;
+  const void* w3;
+  const float* s1; /* per-row fp8 scales; must be NULL for bf16 weights */
+  const float* so;
+  const float* s2;
+  const float* s3;
+  const float* mods;
+  const float* mod_final;
+  const float* rope_cos;
+  const float* rope_sin;
+  const float* w_ain;
+  const float* b_ain;
+  const float* w_aout;
+  const float* b_aout;
+  const void* kvsrc_k; /* KV hand-off source (srows > 0); reserved, must be NULL / 0 */
+  const void* kvsrc_v;
+  int srows;
+  void* kcache;
+  void* vtcache;
+  int Lp;
+  int Lmax;
+  int num_steps;
+  int Tv;
+  int num_layers; /* 18 for pi0.5 */
+  int batch;      /* 1 (batched launches: see fa_pi05_max_batch) */
+  float* x_t;
+  int xt_rows;
+  unsigned long long* stage_cycles; /* optional [16]: per-stage 100 MHz ticks, workgroup 0 */
+  void* workspace;
+  size_t workspace_bytes;
+} fa_pi05_args;
+
+/* Whole S-step Euler loop as ONE cooperative launch (256 workgroups, one per CU). */
+int fa_pi05_denoise(const fa_pi05_args* args, fa_stream_t stream);
+size_t fa_pi05_workspace_bytes(int batch, int Tv, int Lmax);
+/* Zeroes a workspace (required once after allocation and after a non-zero kernel status). */
+int fa_pi05_workspace_init(void* workspace, size_t bytes, fa_stream_t stream);
+/* Synchronous: copies the kernel status bits (FA_KSTATUS_*) of the last launch on this workspace. */
+int fa_pi05_read_status(const void* workspace, unsigned* status);
+int fa_pi05_max_batch(void);
+
+/* ---------------------------------------------------------------- common */
+int fa_device_query(int device, fa_device_info* info);
+const char* fa_last_error(void);
+int fa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FLASHACT_MI355X_H */

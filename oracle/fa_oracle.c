@@ -1,0 +1,441 @@
+/*
+ * fa_oracle.c -- CPU fp32 restatement of the reference's flow-matching denoise loops.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the checker for the MI355X kernels: only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it. The
+ * product path (flashact_amd/) never links, imports or calls it.
+ *
+ * Restated algorithms (reference = /root/reference, read-only):
+ *   pi0.5 action expert, one Euler loop ......... src/pi05/mk6.cu:279-518 (stage order),
+ *       adaRMS + gated residual ................. src/pi05/mk6.cu:137-164, 302, 429, 499-505
+ *       QKV + split-half RoPE ................... src/pi05/mk6.cu:221-244 (pairs j, j+128)
+ *       MQA over prefix + own suffix keys ...... src/pi05/mk6.cu:312-421 (scale 1/16)
+ *       GeLU(tanh)-gated MLP .................... src/pi05/mk6.cu:79-82, 434-497
+ *       final norm + action_out + Euler ......... src/pi05/mk6.cu:502-517 (dt = -1/S)
+ *       time embedding / time MLP / mods ........ src/pi05/hybrid_model.py:111-128,
+ *                                                 src/pi05/pack_weights.py:23-31
+ *       RoPE table .............................. src/pi05/pack_weights.py:54-58
+ *   MolmoAct2 action expert ..................... src/molmoact2/mk_ma2.cu:258-575
+ *       adaLN norm ............................... src/molmoact2/mk_ma2.cu:130-158
+ *       self-attn qk-norm + RoPE (48 pairs) ..... src/molmoact2/mk_ma2.cu:292-381
+ *       cross-attn over per-layer context KV .... src/molmoact2/mk_ma2.cu:397-529
+ *       SiLU-gated MLP ........................... src/molmoact2/mk_ma2.cu:246-251, 542-552
+ *       final layer + masked Euler (dt = +1/S) .. src/molmoact2/mk_ma2.cu:558-571
+ *
+ * Weights use the reference's natural (unpacked) layouts, [out][in] row-major, stored as
+ * bf16 bit patterns (uint16). Every value is converted exactly to fp32 and all arithmetic
+ * is fp32, so the oracle and the GPU path see identical inputs and
+ * differ only in arithmetic precision. Pins: see tests/test_oracle_*.py.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static inline float bf(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static inline float dot_f32(const float* a, const float* b, int n) {
+  /* 8 independent partial sums so the compiler can vectorise without -ffast-math */
+  float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int i = 0;
+  for (; i + 8 <= n; i += 8)
+    for (int j = 0; j < 8; j++) s[j] += a[i + j] * b[i + j];
+  float r = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+  for (; i < n; i++) r += a[i] * b[i];
+  return r;
+}
+
+int fo_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* Y[m][n] = sum_k X[m][k] * W[n][k] (+ bias[n]); W bf16 [N][K]. */
+static void linear_bf16(const float* X, int M, int K, const uint16_t* W, const float* bias, int N, float* Y) {
+#pragma omp parallel
+  {
+    float* wrow = (float*)malloc(sizeof(float) * (size_t)K);
+#pragma omp for schedule(static)
+    for (int n = 0; n < N; n++) {
+      const uint16_t* w = W + (size_t)n * K;
+      for (int k = 0; k < K; k++) wrow[k] = bf(w[k]);
+      float b = bias ? bias[n] : 0.f;
+      for (int m = 0; m < M; m++) Y[(size_t)m * N + n] = dot_f32(X + (size_t)m * K, wrow, K) + b;
+    }
+    free(wrow);
+  }
+}
+
+/* Y[m][n] = sum_k X[m][k] * W[n][k] + bias[n]; W fp32 [N][K]. */
+static void linear_f32(const float* X, int M, int K, const float* W, const float* bias, int N, float* Y) {
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; n++) {
+    float b = bias ? bias[n] : 0.f;
+    for (int m = 0; m < M; m++) Y[(size_t)m * N + n] = dot_f32(X + (size_t)m * K, W + (size_t)n * K, K) + b;
+  }
+}
+
+static inline float silu_f(float x) { return x / (1.0f + expf(-x)); }
+static inline float gelu_tanh_f(float x) {
+  /* GeLU, tanh approximation (Hendrycks & Gimpel 2016), as used by mk6.cu:79-82 */
+  const float k0 = 0.7978845608028654f;
+  return 0.5f * x * (1.0f + tanhf(k0 * (x + 0.044715f * x * x * x)));
+}
+
+/* adaRMS: h = x * rsqrt(mean(x^2) + eps) * (1 + scale) + shift   (mk6.cu:145-161) */
+static void ada_rms(const float* x, int M, int Dm, const float* scale, const float* shift, float* h) {
+  for (int m = 0; m < M; m++) {
+    const float* xr = x + (size_t)m * Dm;
+    float ss = dot_f32(xr, xr, Dm);
+    float r = 1.0f / sqrtf(ss / (float)Dm + 1e-6f);
+    for (int d = 0; d < Dm; d++) h[(size_t)m * Dm + d] = xr[d] * r * (1.0f + scale[d]) + shift[d];
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* pi0.5 time conditioning (hybrid_model.py:111-128)                   */
+/* ------------------------------------------------------------------ */
+
+/* openpi create_sinusoidal_pos_embedding: fraction = linspace(0,1,dim/2) (fp64),
+ * period = min * (max/min)^fraction, freq = 2*pi/period, out = [sin(freq*t), cos(freq*t)]
+ * computed in fp64 and rounded to fp32 (pack_weights.py:26-31). */
+void fo_sinusoid_embedding(const float* t, int n, int dim, double min_period, double max_period, float* out) {
+  int half = dim / 2;
+  for (int i = 0; i < n; i++) {
+    for (int k = 0; k < half; k++) {
+      double frac = (half > 1) ? (double)k / (double)(half - 1) : 0.0;
+      double period = min_period * pow(max_period / min_period, frac);
+      double arg = (1.0 / period * 2.0 * M_PI) * (double)t[i];
+      out[(size_t)i * dim + k] = (float)sin(arg);
+      out[(size_t)i * dim + half + k] = (float)cos(arg);
+    }
+  }
+}
+
+/* mods[s][l][0|1][3D] and mod_final[s][3D] for the fixed schedule t_s = 1 - s/S.
+ * cond = silu(W_to silu(W_ti temb + b_ti) + b_to); mod = W_dense cond + b_dense.
+ * Weights fp32: w_ti/w_to [D][D], w_in/w_post [NL][3D][D], w_fin [3D][D]. */
+void fo_pi05_mods(int S, int NL, int D, const float* w_ti, const float* b_ti, const float* w_to, const float* b_to,
+                  const float* w_in, const float* b_in, const float* w_post, const float* b_post,
+                  const float* w_fin, const float* b_fin, float* mods, float* mod_final) {
+  float* tt = (float*)malloc(sizeof(float) * S);
+  for (int s = 0; s < S; s++) tt[s] = 1.0f - (float)s / (float)S;
+  float* temb = (float*)malloc(sizeof(float) * (size_t)S * D);
+  float* a = (float*)malloc(sizeof(float) * (size_t)S * D);
+  float* cond = (float*)malloc(sizeof(float) * (size_t)S * D);
+  float* m = (float*)malloc(sizeof(float) * (size_t)S * 3 * D);
+  fo_sinusoid_embedding(tt, S, D, 4e-3, 4.0, temb);
+  linear_f32(temb, S, D, w_ti, b_ti, D, a);
+  for (size_t i = 0; i < (size_t)S * D; i++) a[i] = silu_f(a[i]);
+  linear_f32(a, S, D, w_to, b_to, D, cond);
+  for (size_t i = 0; i < (size_t)S * D; i++) cond[i] = silu_f(cond[i]);
+  for (int l = 0; l < NL; l++) {
+    for (int k = 0; k < 2; k++) {
+      const float* W = (k == 0 ? w_in : w_post) + (size_t)l * 3 * D * D;
+      const float* B = (k == 0 ? b_in : b_post) + (size_t)l * 3 * D;
+      linear_f32(cond, S, D, W, B, 3 * D, m);
+      for (int s = 0; s < S; s++)
+        memcpy(mods + (((size_t)s * NL + l) * 2 + k) * 3 * D, m + (size_t)s * 3 * D, sizeof(float) * 3 * D);
+    }
+  }
+  linear_f32(cond, S, D, w_fin, b_fin, 3 * D, mod_final);
+  free(tt); free(temb); free(a); free(cond); free(m);
+}
+
+/* RoPE table (pack_weights.py:54-58): inv_freq_j = 1 / 10000^(2j/HD) in fp32,
+ * angle = pos * inv_freq_j in fp32, pos = start + t. cos/sin [T][HD/2]. */
+void fo_rope_table(int start, int T, int HD, double base, float* cosv, float* sinv) {
+  int half = HD / 2;
+  for (int t = 0; t < T; t++) {
+    float pos = (float)(start + t);
+    for (int j = 0; j < half; j++) {
+      float invf = 1.0f / powf((float)base, (float)(2 * j) / (float)HD);
+      float ang = pos * invf;
+      cosv[(size_t)t * half + j] = cosf(ang);
+      sinv[(size_t)t * half + j] = sinf(ang);
+    }
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* pi0.5 denoise loop (mk6.cu:279-518)                                 */
+/* ------------------------------------------------------------------ */
+typedef struct {
+  int NL, D, H, HD, F, AD;
+  int Lp, Tv, S, batch;
+} fo_pi05_dims;
+
+/* Weights (bf16 bits, natural layouts):
+ *   wq [NL][H*HD][D], wk [NL][HD][D], wv [NL][HD][D], wo [NL][D][H*HD],
+ *   wg [NL][F][D], wu [NL][F][D], wd [NL][D][F]
+ * mods [S][NL][2][3D] (scale|shift|gate), mod_final [S][3D]
+ * rope_cos/sin [Tv][HD/2] for positions Lp + t
+ * w_ain [D][AD], b_ain [D], w_aout [AD][D], b_aout [AD] (fp32)
+ * kpre, vpre [batch][NL][Lp][HD] bf16 (already-RoPE'd prefix keys, values)
+ * x_t [batch][Tv][AD] fp32, updated in place. */
+int fo_pi05_denoise(const fo_pi05_dims* dm, const uint16_t* wq, const uint16_t* wk, const uint16_t* wv,
+                    const uint16_t* wo, const uint16_t* wg, const uint16_t* wu, const uint16_t* wd,
+                    const float* mods, const float* mod_final, const float* rope_cos, const float* rope_sin,
+                    const float* w_ain, const float* b_ain, const float* w_aout, const float* b_aout,
+                    const uint16_t* kpre, const uint16_t* vpre, float* x_t) {
+  const int NL = dm->NL, D = dm->D, H = dm->H, HD = dm->HD, F = dm->F, AD = dm->AD;
+  const int Lp = dm->Lp, Tv = dm->Tv, S = dm->S, B = dm->batch;
+  const int QD = H * HD, half = HD / 2, L = Lp + Tv;
+  if (NL < 1 || D < 1 || H < 1 || HD < 2 || (HD & 1) || F < 1 || AD < 1 || Lp < 0 || Tv < 1 || S < 1 || B < 1) return -1;
+  const float dt = -1.0f / (float)S;
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  float* x = (float*)malloc(sizeof(float) * (size_t)Tv * D);
+  float* h = (float*)malloc(sizeof(float) * (size_t)Tv * D);
+  float* q = (float*)malloc(sizeof(float) * (size_t)Tv * QD);
+  float* k = (float*)malloc(sizeof(float) * (size_t)Tv * HD);
+  float* v = (float*)malloc(sizeof(float) * (size_t)Tv * HD);
+  float* att = (float*)malloc(sizeof(float) * (size_t)Tv * QD);
+  float* o = (float*)malloc(sizeof(float) * (size_t)Tv * D);
+  float* g = (float*)malloc(sizeof(float) * (size_t)Tv * F);
+  float* u = (float*)malloc(sizeof(float) * (size_t)Tv * F);
+  float* Kl = (float*)malloc(sizeof(float) * (size_t)L * HD);
+  float* Vl = (float*)malloc(sizeof(float) * (size_t)L * HD);
+  float* act = (float*)malloc(sizeof(float) * (size_t)Tv * AD);
+
+  for (int b = 0; b < B; b++) {
+    float* xt = x_t + (size_t)b * Tv * AD;
+    for (int s = 0; s < S; s++) {
+      /* embed (mk6.cu:280-288) */
+      linear_f32(xt, Tv, AD, w_ain, b_ain, D, x);
+      for (int l = 0; l < NL; l++) {
+        const float* mod_in = mods + (((size_t)s * NL + l) * 2 + 0) * 3 * D;
+        const float* mod_post = mods + (((size_t)s * NL + l) * 2 + 1) * 3 * D;
+        /* attention block */
+        ada_rms(x, Tv, D, mod_in, mod_in + D, h);
+        linear_bf16(h, Tv, D, wq + (size_t)l * QD * D, NULL, QD, q);
+        linear_bf16(h, Tv, D, wk + (size_t)l * HD * D, NULL, HD, k);
+        linear_bf16(h, Tv, D, wv + (size_t)l * HD * D, NULL, HD, v);
+        for (int t = 0; t < Tv; t++) {
+          const float* c = rope_cos + (size_t)t * half;
+          const float* sn = rope_sin + (size_t)t * half;
+          for (int hh = 0; hh <= H; hh++) {
+            float* vec = (hh < H) ? q + (size_t)t * QD + (size_t)hh * HD : k + (size_t)t * HD;
+            for (int j = 0; j < half; j++) {
+              float a0 = vec[j], a1 = vec[j + half];
+              vec[j] = a0 * c[j] - a1 * sn[j];
+              vec[j + half] = a1 * c[j] + a0 * sn[j];
+            }
+          }
+        }
+        const uint16_t* kp = kpre + (((size_t)b * NL + l) * Lp) * HD;
+        const uint16_t* vp = vpre + (((size_t)b * NL + l) * Lp) * HD;
+        for (size_t i = 0; i < (size_t)Lp * HD; i++) { Kl[i] = bf(kp[i]); Vl[i] = bf(vp[i]); }
+        memcpy(Kl + (size_t)Lp * HD, k, sizeof(float) * (size_t)Tv * HD);
+        memcpy(Vl + (size_t)Lp * HD, v, sizeof(float) * (size_t)Tv * HD);
+#pragma omp parallel
+        {
+          float* p = (float*)malloc(sizeof(float) * (size_t)L);
+#pragma omp for schedule(static)
+          for (int th = 0; th < Tv * H; th++) {
+            int t = th / H, hh = th % H;
+            const float* qv = q + (size_t)t * QD + (size_t)hh * HD;
+            float mx = -INFINITY;
+            for (int j = 0; j < L; j++) {
+              p[j] = dot_f32(qv, Kl + (size_t)j * HD, HD) * scale;
+              if (p[j] > mx) mx = p[j];
+            }
+            float sum = 0.f;
+            for (int j = 0; j < L; j++) { p[j] = expf(p[j] - mx); sum += p[j]; }
+            float inv = 1.0f / sum;
+            float* out = att + (size_t)t * QD + (size_t)hh * HD;
+            for (int d = 0; d < HD; d++) out[d] = 0.f;
+            for (int j = 0; j < L; j++) {
+              float w = p[j] * inv;
+              const float* vr = Vl + (size_t)j * HD;
+              for (int d = 0; d < HD; d++) out[d] += w * vr[d];
+            }
+          }
+          free(p);
+        }
+        linear_bf16(att, Tv, QD, wo + (size_t)l * D * QD, NULL, D, o);
+        for (int t = 0; t < Tv; t++)
+          for (int d = 0; d < D; d++) x[(size_t)t * D + d] += mod_in[2 * D + d] * o[(size_t)t * D + d];
+        /* MLP block */
+        ada_rms(x, Tv, D, mod_post, mod_post + D, h);
+        linear_bf16(h, Tv, D, wg + (size_t)l * F * D, NULL, F, g);
+        linear_bf16(h, Tv, D, wu + (size_t)l * F * D, NULL, F, u);
+        for (size_t i = 0; i < (size_t)Tv * F; i++) g[i] = gelu_tanh_f(g[i]) * u[i];
+        linear_bf16(g, Tv, F, wd + (size_t)l * D * F, NULL, D, o);
+        for (int t = 0; t < Tv; t++)
+          for (int d = 0; d < D; d++) x[(size_t)t * D + d] += mod_post[2 * D + d] * o[(size_t)t * D + d];
+      }
+      /* final norm + action_out + Euler (mk6.cu:502-517) */
+      const float* mf = mod_final + (size_t)s * 3 * D;
+      ada_rms(x, Tv, D, mf, mf + D, h);
+      linear_f32(h, Tv, D, w_aout, b_aout, AD, act);
+      for (size_t i = 0; i < (size_t)Tv * AD; i++) xt[i] += dt * act[i];
+    }
+  }
+  free(x); free(h); free(q); free(k); free(v); free(att); free(o); free(g); free(u);
+  free(Kl); free(Vl); free(act);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* MolmoAct2 flow loop (mk_ma2.cu:258-575)                             */
+/* ------------------------------------------------------------------ */
+typedef struct {
+  int NL, D, H, HD, F, AD;
+  int Lk, Tv, S, adim, batch;
+} fo_ma2_dims;
+
+static void rms_heads(float* v, int M, int H, int HD) {
+  /* per-head RMS norm without weight, eps 1e-6 (mk_ma2.cu:300-315, 403-421) */
+  for (int m = 0; m < M; m++)
+    for (int hh = 0; hh < H; hh++) {
+      float* p = v + (size_t)m * H * HD + (size_t)hh * HD;
+      float r = 1.0f / sqrtf(dot_f32(p, p, HD) / (float)HD + 1e-6f);
+      for (int d = 0; d < HD; d++) p[d] *= r;
+    }
+}
+
+/* softmax(q k^T * scale) v over L keys for each (token, head); K,V [L][H*HD] */
+static void mha(const float* q, int M, int H, int HD, const float* K, const float* V, int L, float scale, float* out) {
+  const int QD = H * HD;
+#pragma omp parallel
+  {
+    float* p = (float*)malloc(sizeof(float) * (size_t)L);
+#pragma omp for schedule(static)
+    for (int th = 0; th < M * H; th++) {
+      int t = th / H, hh = th % H;
+      const float* qv = q + (size_t)t * QD + (size_t)hh * HD;
+      float mx = -INFINITY;
+      for (int j = 0; j < L; j++) {
+        p[j] = dot_f32(qv, K + (size_t)j * QD + (size_t)hh * HD, HD) * scale;
+        if (p[j] > mx) mx = p[j];
+      }
+      float sum = 0.f;
+      for (int j = 0; j < L; j++) { p[j] = expf(p[j] - mx); sum += p[j]; }
+      float inv = 1.0f / sum;
+      float* o = out + (size_t)t * QD + (size_t)hh * HD;
+      for (int d = 0; d < HD; d++) o[d] = 0.f;
+      for (int j = 0; j < L; j++) {
+        float w = p[j] * inv;
+        const float* vr = V + (size_t)j * QD + (size_t)hh * HD;
+        for (int d = 0; d < HD; d++) o[d] += w * vr[d];
+      }
+    }
+    free(p);
+  }
+}
+
+/* Weights (bf16 bits, natural layouts, fp32 biases):
+ *   w_qkv [NL][3D][D] + b_qkv [NL][3D] (rows q | k | v), w_so [NL][D][D] + b_so,
+ *   w_cq + b_cq, w_co + b_co, w_g/w_u [NL][F][D] + b_g/b_u [NL][F], w_dn [NL][D][F] + b_dn
+ * mods [S][NL][3][3][D] ({msa,mca,mlp} x {scale,shift,gate}), mod_final [S][2][D] (scale, shift)
+ * rope_cos/sin [Tv][HD/2] (positions 0..Tv-1, split-half pairs d, d+HD/2)
+ * w_ain [D][AD] fp32 + b_ain, w_aout [AD][D] bf16 + b_aout fp32
+ * kctx, vctx [batch][NL][Lk][D] bf16 (projected, normed cross K; cross V)
+ * x_t [batch][Tv][AD] fp32 in/out; only dims < adim are updated. */
+int fo_ma2_flow(const fo_ma2_dims* dm, const uint16_t* w_qkv, const float* b_qkv, const uint16_t* w_so,
+                const float* b_so, const uint16_t* w_cq, const float* b_cq, const uint16_t* w_co, const float* b_co,
+                const uint16_t* w_g, const float* b_g, const uint16_t* w_u, const float* b_u, const uint16_t* w_dn,
+                const float* b_dn, const float* mods, const float* mod_final, const float* rope_cos,
+                const float* rope_sin, const float* w_ain, const float* b_ain, const uint16_t* w_aout,
+                const float* b_aout, const uint16_t* kctx, const uint16_t* vctx, float* x_t) {
+  const int NL = dm->NL, D = dm->D, H = dm->H, HD = dm->HD, F = dm->F, AD = dm->AD;
+  const int Lk = dm->Lk, Tv = dm->Tv, S = dm->S, adim = dm->adim, B = dm->batch;
+  const int half = HD / 2;
+  if (NL < 1 || D < 1 || H < 1 || HD < 2 || (HD & 1) || H * HD != D || F < 1 || AD < 1 || Lk < 1 || Tv < 1 ||
+      S < 1 || adim < 0 || adim > AD || B < 1)
+    return -1;
+  const float dt = 1.0f / (float)S;
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  float* x = (float*)malloc(sizeof(float) * (size_t)Tv * D);
+  float* h = (float*)malloc(sizeof(float) * (size_t)Tv * D);
+  float* qkv = (float*)malloc(sizeof(float) * (size_t)Tv * 3 * D);
+  float* q = (float*)malloc(sizeof(float) * (size_t)Tv * D);
+  float* k = (float*)malloc(sizeof(float) * (size_t)Tv * D);
+  float* v = (float*)malloc(sizeof(float) * (size_t)Tv * D);
+  float* att = (float*)malloc(sizeof(float) * (size_t)Tv * D);
+  float* o = (float*)malloc(sizeof(float) * (size_t)Tv * D);
+  float* gg = (float*)malloc(sizeof(float) * (size_t)Tv * F);
+  float* uu = (float*)malloc(sizeof(float) * (size_t)Tv * F);
+  float* Kc = (float*)malloc(sizeof(float) * (size_t)Lk * D);
+  float* Vc = (float*)malloc(sizeof(float) * (size_t)Lk * D);
+  float* wa = (float*)malloc(sizeof(float) * (size_t)AD * D);
+  float* act = (float*)malloc(sizeof(float) * (size_t)Tv * AD);
+  for (size_t i = 0; i < (size_t)AD * D; i++) wa[i] = bf(w_aout[i]);
+
+  for (int b = 0; b < B; b++) {
+    float* xt = x_t + (size_t)b * Tv * AD;
+    for (int s = 0; s < S; s++) {
+      linear_f32(xt, Tv, AD, w_ain, b_ain, D, x); /* mk_ma2.cu:259-268 */
+      for (int l = 0; l < NL; l++) {
+        const float* ml = mods + ((size_t)s * NL + l) * 9 * D;
+        const float *sc_msa = ml, *sh_msa = ml + D, *g_msa = ml + 2 * D;
+        const float *sc_mca = ml + 3 * D, *sh_mca = ml + 4 * D, *g_mca = ml + 5 * D;
+        const float *sc_mlp = ml + 6 * D, *sh_mlp = ml + 7 * D, *g_mlp = ml + 8 * D;
+        /* self attention */
+        ada_rms(x, Tv, D, sc_msa, sh_msa, h);
+        linear_bf16(h, Tv, D, w_qkv + (size_t)l * 3 * D * D, b_qkv + (size_t)l * 3 * D, 3 * D, qkv);
+        for (int t = 0; t < Tv; t++) {
+          memcpy(q + (size_t)t * D, qkv + (size_t)t * 3 * D, sizeof(float) * D);
+          memcpy(k + (size_t)t * D, qkv + (size_t)t * 3 * D + D, sizeof(float) * D);
+          memcpy(v + (size_t)t * D, qkv + (size_t)t * 3 * D + 2 * D, sizeof(float) * D);
+        }
+        rms_heads(q, Tv, H, HD);
+        rms_heads(k, Tv, H, HD);
+        for (int t = 0; t < Tv; t++) {
+          const float* c = rope_cos + (size_t)t * half;
+          const float* sn = rope_sin + (size_t)t * half;
+          for (int hh = 0; hh < H; hh++)
+            for (int which = 0; which < 2; which++) {
+              float* vec = (which == 0 ? q : k) + (size_t)t * D + (size_t)hh * HD;
+              for (int j = 0; j < half; j++) {
+                float a0 = vec[j], a1 = vec[j + half];
+                vec[j] = a0 * c[j] - a1 * sn[j];
+                vec[j + half] = a0 * sn[j] + a1 * c[j];
+              }
+            }
+        }
+        mha(q, Tv, H, HD, k, v, Tv, scale, att);
+        linear_bf16(att, Tv, D, w_so + (size_t)l * D * D, b_so + (size_t)l * D, D, o);
+        for (size_t i = 0; i < (size_t)Tv * D; i++) x[i] += g_msa[i % D] * o[i];
+        /* cross attention */
+        ada_rms(x, Tv, D, sc_mca, sh_mca, h);
+        linear_bf16(h, Tv, D, w_cq + (size_t)l * D * D, b_cq + (size_t)l * D, D, q);
+        rms_heads(q, Tv, H, HD);
+        const uint16_t* kc = kctx + (((size_t)b * NL + l) * Lk) * D;
+        const uint16_t* vc = vctx + (((size_t)b * NL + l) * Lk) * D;
+        for (size_t i = 0; i < (size_t)Lk * D; i++) { Kc[i] = bf(kc[i]); Vc[i] = bf(vc[i]); }
+        mha(q, Tv, H, HD, Kc, Vc, Lk, scale, att);
+        linear_bf16(att, Tv, D, w_co + (size_t)l * D * D, b_co + (size_t)l * D, D, o);
+        for (size_t i = 0; i < (size_t)Tv * D; i++) x[i] += g_mca[i % D] * o[i];
+        /* MLP */
+        ada_rms(x, Tv, D, sc_mlp, sh_mlp, h);
+        linear_bf16(h, Tv, D, w_g + (size_t)l * F * D, b_g + (size_t)l * F, F, gg);
+        linear_bf16(h, Tv, D, w_u + (size_t)l * F * D, b_u + (size_t)l * F, F, uu);
+        for (size_t i = 0; i < (size_t)Tv * F; i++) gg[i] = silu_f(gg[i]) * uu[i];
+        linear_bf16(gg, Tv, F, w_dn + (size_t)l * D * F, b_dn + (size_t)l * D, D, o);
+        for (size_t i = 0; i < (size_t)Tv * D; i++) x[i] += g_mlp[i % D] * o[i];
+      }
+      const float* mf = mod_final + (size_t)s * 2 * D;
+      ada_rms(x, Tv, D, mf, mf + D, h);
+      linear_f32(h, Tv, D, wa, b_aout, AD, act);
+      for (int t = 0; t < Tv; t++)
+        for (int a = 0; a < adim; a++) xt[(size_t)t * AD + a] += dt * act[(size_t)t * AD + a];
+    }
+  }
+  free(x); free(h); free(qkv); free(q); free(k); free(v); free(att); free(o); free(gg); free(uu);
+  free(Kc); free(Vc); free(wa); free(act);
+  return 0;
+}

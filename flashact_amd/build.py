@@ -3,6 +3,7 @@ from __future__ import annotations
 
 import glob
 import os
+import re
 import subprocess
 import sys
 
@@ -19,11 +20,25 @@ HIPCC_FLAGS = [
 ]
 
 
+# hipcc (ROCm 7.2) evaluates __builtin_bit_cast(T, v[i]) on an ext_vector element as a cast of
+# element 0; kernels use as_f32/as_u32 (fa_device.h) instead, and the build rejects the direct form.
+BAD_BITCAST = re.compile(r"__builtin_bit_cast\(\s*[\w:]+\s*,\s*[^(),]*\[")
+
+
+def check_sources() -> None:
+    for src in sources() + sorted(glob.glob(os.path.join(HERE, "csrc", "*.h"))):
+        for no, line in enumerate(open(src), 1):
+            if BAD_BITCAST.search(line.split("//", 1)[0]):
+                raise RuntimeError(f"{src}:{no}: __builtin_bit_cast of a vector element is mis-compiled; "
+                                   f"use as_f32/as_u32: {line.strip()}")
+
+
 def sources():
     return sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")))
 
 
 def build(verbose: bool = False) -> str:
+    check_sources()
     os.makedirs(LIB_DIR, exist_ok=True)
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
     tmp = LIB_PATH + ".tmp"

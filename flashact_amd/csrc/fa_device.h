@@ -75,6 +75,11 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                  0, 0);
 }
 
+// hipcc (ROCm 7.2, clang 22) evaluates __builtin_bit_cast(T, v[i]) on an element of an
+// ext_vector_type as a cast of element 0. Element reinterpretation therefore goes through
+// these value-parameter helpers; flashact_amd/build.py rejects the direct form in csrc/.
+__device__ __forceinline__ float as_f32(unsigned u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ unsigned as_u32(float f) { return __builtin_bit_cast(unsigned, f); }
 __device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
 __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
   bf16x2 v = {(bf16)a, (bf16)b};

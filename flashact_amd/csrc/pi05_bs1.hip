@@ -416,8 +416,8 @@ __device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c) {
     float mc = -1e30f, lc = 0.f;
     if (t < p.Tv) {
       const u32x2 v = ldb64<kCpSc1>(c.ws, OFF_ATTML + (((c.g * NCH + ch) * TP + t) * 2) * 4);
-      mc = __builtin_bit_cast(float, v[0]);
-      lc = __builtin_bit_cast(float, v[1]);
+      mc = as_f32(v[0]);
+      lc = as_f32(v[1]);
     }
     float M = mc;
 #pragma unroll

@@ -80,6 +80,8 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 // these value-parameter helpers; flashact_amd/build.py rejects the direct form in csrc/.
 __device__ __forceinline__ float as_f32(unsigned u) { return __builtin_bit_cast(float, u); }
 __device__ __forceinline__ unsigned as_u32(float f) { return __builtin_bit_cast(unsigned, f); }
+__device__ __forceinline__ f32x4 as_f32x4(u32x4 u) { return __builtin_bit_cast(f32x4, u); }
+__device__ __forceinline__ u32x4 as_u32x4(f32x4 f) { return __builtin_bit_cast(u32x4, f); }
 __device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
 __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
   bf16x2 v = {(bf16)a, (bf16)b};

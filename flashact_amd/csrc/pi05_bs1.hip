@@ -31,6 +31,7 @@ constexpr int D = 1024, HD = 256, AD = 32;
 constexpr int NX = 8, NR = 32, NWG = 256, NTH = 256, TP = 64;
 constexpr int NCH = 32;  // attention key chunks per head (= ranks)
 constexpr uint32_t LDS_BYTES = 96 * 1024;  // > 80 KB forces one workgroup per CU
+constexpr uint32_t OOB = 0x80000000u;      // buffer offset past every resource: loads return 0
 
 // workspace layout (bytes)
 constexpr uint32_t OFF_CTRL = 0;          // u64 seq, u32 err
@@ -38,9 +39,7 @@ constexpr uint32_t OFF_XFLAG = 256;       // [8][32] u64
 constexpr uint32_t OFF_GFLAG = 2304;      // [8] u64
 constexpr uint32_t OFF_XN = 4096;                                   // [8][64][1024] bf16
 constexpr uint32_t OFF_Q = OFF_XN + NX * TP * D * 2;                // [8][64][256] bf16
-constexpr uint32_t OFF_KS = OFF_Q + NX * TP * HD * 2;               // [8][64][256] bf16
-constexpr uint32_t OFF_VTS = OFF_KS + NX * TP * HD * 2;             // [8][256][64] bf16
-constexpr uint32_t OFF_ATTP = OFF_VTS + NX * HD * TP * 2;           // [8][32][64][256] f32
+constexpr uint32_t OFF_ATTP = OFF_Q + NX * TP * HD * 2;             // [8][32][64][256] f32
 constexpr uint32_t OFF_ATTML = OFF_ATTP + NX * NCH * TP * HD * 4;   // [8][32][64][2] f32
 constexpr uint32_t OFF_ATTN = OFF_ATTML + NX * NCH * TP * 2 * 4;    // [8][64][256] bf16
 constexpr uint32_t OFF_H = OFF_ATTN + NX * TP * HD * 2;             // [8][64][512] bf16
@@ -88,7 +87,7 @@ struct Ctx {
 __device__ __forceinline__ void mark(const Params& p, const Ctx& c, int idx, uint64_t& t0) {
   if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x == 0) {
     uint64_t now = __builtin_amdgcn_s_memrealtime();
-    p.stage_cycles[idx] += now - t0;
+    p.stage_cycles[idx] += now - t0;  // slots 0-8: stage work, 9: XCD waits, 10: grid waits
     t0 = now;
   }
 }
@@ -103,10 +102,9 @@ __device__ __forceinline__ void gemm_core(f32x4 (&acc)[RT][4], const u32x4 (&wf)
   u32x4 xf[4][KS];
 #pragma unroll
   for (int tt = 0; tt < 4; tt++) {
-    const bool ok = tt * 16 + c.lr < Tv;
+    const uint32_t base = tt * 16 + c.lr < Tv ? xoff + tt * 16 * xrow : OOB;
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++)
-      xf[tt][ks] = ok ? ldb128<kCpSc1>(c.ws, xoff + tt * 16 * xrow + ks * 64) : u32x4{0, 0, 0, 0};
+    for (int ks = 0; ks < KS; ks++) xf[tt][ks] = ldb128<kCpSc1>(c.ws, base + ks * 64);
   }
 #pragma unroll
   for (int rt = 0; rt < RT; rt++)
@@ -150,6 +148,16 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, uint32
   const int d0 = c.tid * 4;
   f32x4 xv[2];
   float ss[2];
+  u32x4 part[2][NX];
+  if (MODE != 0) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int t = c.r + 32 * j;
+#pragma unroll
+      for (int gg = 0; gg < NX; gg++)
+        part[j][gg] = ldb128<kCpSc1>(c.ws, t < p.Tv ? part_off + ((gg * TP + t) * D + d0) * 4 : OOB);
+    }
+  }
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     const int t = c.r + 32 * j;
@@ -165,10 +173,9 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, uint32
           v[i] = a;
         }
       } else {
-        f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+        f32x4 sum = as_f32x4(part[j][0]);
 #pragma unroll
-        for (int gg = 0; gg < NX; gg++)
-          sum += __builtin_bit_cast(f32x4, ldb128<kCpSc1>(c.ws, part_off + ((gg * TP + t) * D + d0) * 4));
+        for (int gg = 1; gg < NX; gg++) sum += as_f32x4(part[j][gg]);
         const f32x4 gt = *reinterpret_cast<const f32x4*>(gate + d0);
         const f32x4 xo = *reinterpret_cast<const f32x4*>(xres + j * D + d0);
         v = xo + gt * sum;
@@ -266,29 +273,29 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
       const float lo0 = v[0] * cs[0] - v[1] * sn[0], hi0 = v[1] * cs[0] + v[0] * sn[0];
       const float lo1 = v[2] * cs[1] - v[3] * sn[1], hi1 = v[3] * cs[1] + v[2] * sn[1];
       const unsigned plo = pack_bf16x2(lo0, lo1), phi = pack_bf16x2(hi0, hi1);
-      const uint32_t off = (vr0 < 256 ? OFF_Q : OFF_KS) + ((c.g * TP + t) * HD + j) * 2;
-      *reinterpret_cast<unsigned*>(p.ws + off) = plo;
-      *reinterpret_cast<unsigned*>(p.ws + off + 256) = phi;
-      if (vr0 >= 256 && c.g == 0) {  // suffix keys into the caller's cache (reference contract)
+      if (vr0 < 256) {
+        const uint32_t off = OFF_Q + ((c.g * TP + t) * HD + j) * 2;
+        *reinterpret_cast<unsigned*>(p.ws + off) = plo;
+        *reinterpret_cast<unsigned*>(p.ws + off + 256) = phi;
+      } else {
+        // Suffix keys go to the caller's cache (the reference's output contract). Every XCD
+        // writes the same values and reads back its own L2 copy in the attention stage.
         bf16* kr = p.kcache + ((size_t)l * p.Lmax + p.Lp + t) * HD;
         *reinterpret_cast<unsigned*>(kr + j) = plo;
         *reinterpret_cast<unsigned*>(kr + j + 128) = phi;
       }
     } else {
       const int d = vr0 - 512;
-      bf16* vts = reinterpret_cast<bf16*>(p.ws + OFF_VTS) + (c.g * HD + d) * TP + t;
+      bf16* vr = p.vtcache + ((size_t)l * HD + d) * p.Lmax + p.Lp + t;
 #pragma unroll
-      for (int i = 0; i < 4; i++) vts[i * TP] = (bf16)v[i];
-      if (c.g == 0) {
-        bf16* vr = p.vtcache + ((size_t)l * HD + d) * p.Lmax + p.Lp + t;
-#pragma unroll
-        for (int i = 0; i < 4; i++) vr[(size_t)i * p.Lmax] = (bf16)v[i];
-      }
+      for (int i = 0; i < 4; i++) vr[(size_t)i * p.Lmax] = (bf16)v[i];
     }
   }
 }
 
 // ---------------------------------------------------------------- attention partials
+// Head g, keys [r*C, r*C+C): prefix keys and this step's suffix keys both come from the caches.
+// Per 32-key block every K row fragment and V^T fragment is issued before the first MFMA.
 __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l) {
   const int Ltot = p.Lp + p.Tv;
   const int C = 32 * ((Ltot + 32 * NCH - 1) / (32 * NCH));
@@ -299,37 +306,60 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l) 
   const float qscale = 1.4426950408889634f / 16.0f;  // log2(e) / sqrt(256)
 
   u32x4 qf[8];
+  {
+    const uint32_t qb = tok_ok ? OFF_Q + ((c.g * TP + t) * HD + c.lq * 8) * 2 : OOB;
 #pragma unroll
-  for (int ks = 0; ks < 8; ks++)
-    qf[ks] = tok_ok ? ldb128<kCpSc1>(c.ws, OFF_Q + ((c.g * TP + t) * HD + ks * 32 + c.lq * 8) * 2) : u32x4{0, 0, 0, 0};
-
+    for (int ks = 0; ks < 8; ks++) qf[ks] = ldb128<kCpSc1>(c.ws, qb + ks * 64);
+  }
   float m = -1e30f, lsum = 0.f;
   f32x4 o[16];
 #pragma unroll
   for (int dt = 0; dt < 16; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const uint32_t kc_layer = (uint32_t)l * p.Lmax * HD * 2;
+  const uint32_t kl = (uint32_t)l * p.Lmax * HD * 2;  // layer base, kcache [Lmax][256]
+  const uint32_t vl = (uint32_t)l * HD * p.Lmax * 2;  // layer base, vtcache [256][Lmax]
 #pragma unroll 1
   for (int kb = kbeg; kb < kend; kb += 32) {
-    f32x4 s[2];
+    u32x4 kf[2][8];
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
       const int key = kb + kt * 16 + c.lr;
-      u32x4 kf[8];
+      const uint32_t rb = key < kend ? kl + key * HD * 2 + c.lq * 16 : OOB;
 #pragma unroll
-      for (int ks = 0; ks < 8; ks++) {
-        const uint32_t dk = (ks * 32 + c.lq * 8) * 2;
-        if (key < p.Lp)
-          kf[ks] = ldb128<kCpPlain>(c.kc, kc_layer + key * HD * 2 + dk);
-        else if (key < Ltot)
-          kf[ks] = ldb128<kCpSc1>(c.ws, OFF_KS + (c.g * TP + (key - p.Lp)) * HD * 2 + dk);
-        else
-          kf[ks] = u32x4{0, 0, 0, 0};
-      }
+      for (int ks = 0; ks < 8; ks++) kf[kt][ks] = ldb128<kCpSc1>(c.kc, rb + ks * 64);
+    }
+    // V^T fragments: dim 16dt+lr, keys kg0 = kb+4lq+(0..3) and kg1 = kb+16+4lq+(0..3).
+    // The first half is issued with K; the second after the S MFMAs release the K registers.
+    const int kg0 = kb + c.lq * 4, kg1 = kg0 + 16;
+    const uint32_t vo0 = kg0 < kend ? vl + c.lr * p.Lmax * 2 + kg0 * 2 : OOB;
+    const uint32_t vo1 = kg1 < kend ? vl + c.lr * p.Lmax * 2 + kg1 * 2 : OOB;
+    const uint32_t vstep = 16 * p.Lmax * 2;  // 16 dims
+    u32x2 vf[16][2];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) {
+      vf[dt][0] = ldb64<kCpSc1>(c.vc, vo0 + (vo0 == OOB ? 0 : dt * vstep));
+      vf[dt][1] = ldb64<kCpSc1>(c.vc, vo1 + (vo1 == OOB ? 0 : dt * vstep));
+    }
+    // zero V elements of keys >= kend inside a partially valid 4-key group
+    unsigned vm[2][2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; h2++) {
+      const int nv = min(max(kend - (h2 ? kg1 : kg0), 0), 4);
+      vm[h2][0] = nv >= 2 ? 0xffffffffu : (nv == 1 ? 0xffffu : 0u);
+      vm[h2][1] = nv >= 4 ? 0xffffffffu : (nv == 3 ? 0xffffu : 0u);
+    }
+    f32x4 s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
       f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 8; ks++) a = mfma16(kf[ks], qf[ks], a);
+      for (int ks = 0; ks < 8; ks++) a = mfma16(kf[kt][ks], qf[ks], a);
       s[kt] = a;
+    }
+#pragma unroll
+    for (int dt = 8; dt < 16; dt++) {
+      vf[dt][0] = ldb64<kCpSc1>(c.vc, vo0 + (vo0 == OOB ? 0 : dt * vstep));
+      vf[dt][1] = ldb64<kCpSc1>(c.vc, vo1 + (vo1 == OOB ? 0 : dt * vstep));
     }
     // lane holds S^T[key kb + 16kt + 4lq + i][token lr]
     float bmax = -1e30f;
@@ -362,37 +392,13 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l) 
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);
     lsum = lsum * alpha + psum;
-    // B operand P^T: k-slot 8lq+i <-> key kb+4lq+i (i<4), kb+16+4lq+(i-4) (i>=4)
+    // B operand P^T: k-slot 8lq+i <-> key kg0+i (i<4), kg1+(i-4) (i>=4)
     const u32x4 pb = {pk[0], pk[1], pk[2], pk[3]};
-    const int kg0 = kb + c.lq * 4, kg1 = kb + 16 + c.lq * 4;
 #pragma unroll
     for (int dt = 0; dt < 16; dt++) {
-      const int dim = dt * 16 + c.lr;
-      u32x4 vf;
-#pragma unroll
-      for (int h2 = 0; h2 < 2; h2++) {
-        const int kg = h2 ? kg1 : kg0;
-        u32x2 vv;
-        if (kg + 3 < p.Lp) {
-          vv = ldb64<kCpPlain>(c.vc, (((uint32_t)l * HD + dim) * p.Lmax + kg) * 2);
-        } else {
-          unsigned short e4[4];
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const int key = kg + i;
-            if (key < p.Lp)
-              e4[i] = ldb16<kCpPlain>(c.vc, (((uint32_t)l * HD + dim) * p.Lmax + key) * 2);
-            else if (key < Ltot)
-              e4[i] = ldb16<kCpSc1>(c.ws, OFF_VTS + ((c.g * HD + dim) * TP + (key - p.Lp)) * 2);
-            else
-              e4[i] = 0;
-          }
-          vv = u32x2{(unsigned)e4[0] | ((unsigned)e4[1] << 16), (unsigned)e4[2] | ((unsigned)e4[3] << 16)};
-        }
-        vf[h2 * 2 + 0] = vv[0];
-        vf[h2 * 2 + 1] = vv[1];
-      }
-      o[dt] = mfma16(vf, pb, o[dt] * alpha);
+      const u32x4 va = {vf[dt][0][0] & vm[0][0], vf[dt][0][1] & vm[0][1], vf[dt][1][0] & vm[1][0],
+                        vf[dt][1][1] & vm[1][1]};
+      o[dt] = mfma16(va, pb, o[dt] * alpha);
     }
   }
   // lane holds O^T[dim 16dt + 4lq + i][token lr]
@@ -408,17 +414,16 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l) 
 }
 
 // ---------------------------------------------------------------- combine
+// attn_g[t] = sum_ch 2^(m_ch - M) O_ch[t] / sum_ch 2^(m_ch - M) l_ch for my tokens r, r+32.
 __device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c) {
   float* cw = c.lds + L_CW;
+  float* red2 = reinterpret_cast<float*>(c.red);  // [4 chunk groups][2 tokens][256]
   if (c.tid < 64) {
     const int j = c.tid >> 5, ch = c.tid & 31;
     const int t = c.r + 32 * j;
-    float mc = -1e30f, lc = 0.f;
-    if (t < p.Tv) {
-      const u32x2 v = ldb64<kCpSc1>(c.ws, OFF_ATTML + (((c.g * NCH + ch) * TP + t) * 2) * 4);
-      mc = as_f32(v[0]);
-      lc = as_f32(v[1]);
-    }
+    const u32x2 v = ldb64<kCpSc1>(c.ws, t < p.Tv ? OFF_ATTML + (((c.g * NCH + ch) * TP + t) * 2) * 4 : OOB);
+    const float mc = t < p.Tv ? as_f32(v[0]) : -1e30f;
+    const float lc = as_f32(v[1]);
     float M = mc;
 #pragma unroll
     for (int o = 16; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
@@ -428,16 +433,34 @@ __device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c) {
     for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
     cw[j * 32 + ch] = (t < p.Tv) ? wgt / L : 0.f;
   }
-  __syncthreads();
+  const int q = c.tid & 63, cg = c.tid >> 6;  // dims 4q..4q+3, chunks 8cg..8cg+7
+  u32x4 buf[2][8];
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     const int t = c.r + 32 * j;
-    if (t >= p.Tv) continue;
-    float acc = 0.f;
-#pragma unroll 8
-    for (int ch = 0; ch < NCH; ch++)
-      acc += cw[j * 32 + ch] * ldbf32<kCpSc1>(c.ws, OFF_ATTP + (((c.g * NCH + ch) * TP + t) * HD + c.tid) * 4);
-    reinterpret_cast<bf16*>(p.ws + OFF_ATTN)[(c.g * TP + t) * HD + c.tid] = (bf16)acc;
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      buf[j][k] = ldb128<kCpSc1>(
+          c.ws, t < p.Tv ? OFF_ATTP + (((c.g * NCH + cg * 8 + k) * TP + t) * HD + 4 * q) * 4 : OOB);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc += cw[j * 32 + cg * 8 + k] * as_f32x4(buf[j][k]);
+    *reinterpret_cast<f32x4*>(red2 + (cg * 2 + j) * HD + 4 * q) = acc;
+  }
+  __syncthreads();
+  if (c.tid < 128) {
+    const int j = c.tid >> 6, t = c.r + 32 * j;
+    if (t < p.Tv) {
+      f32x4 a = *reinterpret_cast<const f32x4*>(red2 + (0 * 2 + j) * HD + 4 * q);
+#pragma unroll
+      for (int g2 = 1; g2 < 4; g2++) a += *reinterpret_cast<const f32x4*>(red2 + (g2 * 2 + j) * HD + 4 * q);
+      const u32x2 pk = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+      *reinterpret_cast<u32x2*>(p.ws + OFF_ATTN + ((c.g * TP + t) * HD + 4 * q) * 2) = pk;
+    }
   }
 }
 
@@ -461,7 +484,7 @@ __device__ __forceinline__ void stage_oproj(const Params& p, const Ctx& c, const
     const f32x4 v = reduce_get<2>(c, rt);
     if (t < p.Tv)
       stb128<kCpSc1>(c.ws, OFF_OPART + ((c.g * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 4,
-                     __builtin_bit_cast(u32x4, v));
+                     as_u32x4(v));
   }
 }
 
@@ -510,7 +533,7 @@ __device__ __forceinline__ void stage_dn(const Params& p, const Ctx& c, const u3
     const f32x4 v = reduce_get<2>(c, rt);
     if (t < p.Tv)
       stb128<kCpSc1>(c.ws, OFF_ZPART + ((c.g * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 4,
-                     __builtin_bit_cast(u32x4, v));
+                     as_u32x4(v));
   }
 }
 
@@ -572,15 +595,18 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
         sync_arrive(s);
         load_w_qkv(p, c, l, w);
         sync_wait_xcd(s);
+        mark(p, c, 9, t0);
         stage_qkv(p, c, l, w);
       }
       mark(p, c, 1, t0);
       sync_arrive(s);
       sync_wait_xcd(s);
+      mark(p, c, 9, t0);
       stage_att(p, c, l);
       mark(p, c, 2, t0);
       sync_arrive(s);
       sync_wait_xcd(s);
+      mark(p, c, 9, t0);
       stage_comb(p, c);
       mark(p, c, 3, t0);
       {
@@ -588,11 +614,13 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
         sync_arrive(s);
         load_w_o(p, c, l, w);
         sync_wait_xcd(s);
+        mark(p, c, 9, t0);
         stage_oproj(p, c, w);
       }
       mark(p, c, 4, t0);
       sync_arrive(s);
       sync_wait_grid(s);
+      mark(p, c, 10, t0);
       stage_norm<1>(p, c, OFF_OPART, mod_in + 2 * D, mod_post, mod_post + D);
       mark(p, c, 5, t0);
       {
@@ -600,6 +628,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
         sync_arrive(s);
         load_w_gu(p, c, l, w);
         sync_wait_xcd(s);
+        mark(p, c, 9, t0);
         stage_gu(p, c, w);
       }
       mark(p, c, 6, t0);
@@ -608,11 +637,13 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
         sync_arrive(s);
         load_w_dn(p, c, l, w);
         sync_wait_xcd(s);
+        mark(p, c, 9, t0);
         stage_dn(p, c, w);
       }
       mark(p, c, 7, t0);
       sync_arrive(s);
       sync_wait_grid(s);
+      mark(p, c, 10, t0);
     }
     const float* gl = p.mods + ((size_t)(step * NL + NL - 1) * 2 + 1) * 3 * D + 2 * D;
     const float* mf = p.mod_final + (size_t)step * 3 * D;

@@ -1,0 +1,88 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol include/flashact_mi355x.h declares,
+and its argument validation rejects bad requests before touching a device (no kernel launches)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from flashact_amd import _lib
+from flashact_amd.build import LIB_PATH
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flashact_mi355x.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*[A-Za-z_][\w \*]*?\b(fa_\w+)\s*\(", src, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB_PATH):
+        from flashact_amd import build
+        build.build()
+    return _lib.lib()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = _declared()
+    assert "fa_pi05_denoise" in names and len(names) >= 8
+    so = ctypes.CDLL(LIB_PATH)
+    for n in names:
+        assert hasattr(so, n), f"{n} declared in the header but not exported"
+    assert sorted(n for n, _, _ in _lib.SYMBOLS) == names, "ctypes binding out of sync with the header"
+
+
+def test_versions_and_sizes(lib):
+    assert lib.fa_abi_version() == _lib.ABI_VERSION
+    assert lib.fa_pi05_max_batch() >= 1
+    ws = lib.fa_pi05_workspace_bytes(1, 50, 1024)
+    assert ws > 0 and ws % 256 == 0
+
+
+def _args(**kw):
+    a = _lib.Pi05Args()
+    fake = 1 << 20  # aligned dummy addresses: validation must fail before anything is dereferenced
+    for f in ("w1", "wo", "w2", "w3", "mods", "mod_final", "rope_cos", "rope_sin", "w_ain", "b_ain", "w_aout",
+              "b_aout", "kcache", "vtcache", "x_t", "workspace"):
+        setattr(a, f, fake)
+    a.Lp, a.Lmax, a.num_steps, a.Tv, a.num_layers, a.batch, a.xt_rows = 968, 1024, 10, 50, 18, 1, 50
+    a.workspace_bytes = 1 << 30
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code,text", [
+    (dict(Tv=65, xt_rows=65), 1, "Tv"),
+    (dict(Tv=0), 1, "Tv"),
+    (dict(Lmax=1000), 1, "Lmax"),
+    (dict(Lmax=1008), 1, "Lmax"),
+    (dict(xt_rows=10), 1, "xt_rows"),
+    (dict(workspace_bytes=4096), 1, "workspace"),
+    (dict(w2=None), 1, "w2 is NULL"),
+    (dict(kcache=(1 << 20) + 8), 1, "kcache is not 16-byte aligned"),
+    (dict(srows=4), 2, "hand-off"),
+    (dict(weight_dtype=1), 2, "bf16"),
+    (dict(batch=3), 2, "batch"),
+])
+def test_denoise_rejects_bad_requests(lib, kw, code, text):
+    rc = lib.fa_pi05_denoise(ctypes.byref(_args(**kw)), None)
+    assert rc == code
+    assert text in lib.fa_last_error().decode()
+
+
+def test_denoise_null_args(lib):
+    assert lib.fa_pi05_denoise(None, None) == 1
+    assert "NULL" in lib.fa_last_error().decode()
+
+
+def test_denoise_without_device(lib):
+    """A valid request on a host without an MI355X fails with FA_ERR_DEVICE and launches nothing."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    assert lib.fa_pi05_denoise(ctypes.byref(_args()), None) == 3

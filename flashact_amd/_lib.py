@@ -38,6 +38,7 @@ class Pi05Args(ctypes.Structure):
         ("x_t", ctypes.c_void_p), ("xt_rows", ctypes.c_int),
         ("stage_cycles", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("trace", ctypes.c_void_p), ("trace_layer", ctypes.c_int),
     ]
 
 

@@ -1,25 +1,36 @@
 // pi0.5 action-expert denoise loop, batch 1: the whole S-step Euler loop in ONE cooperative
-// launch of 256 workgroups (one per CU) x 256 threads (4 waves, one per SIMD) on gfx950.
+// launch of 256 workgroups (one per CU) on gfx950. Each workgroup runs 6 waves:
+//   waves 0-3  compute waves. Each is an independent agent: it owns token tile w (tokens
+//              16w..16w+15) in every GEMM and attention stage and signals its own barrier flag,
+//              so no workgroup barrier is executed after the prologue.
+//   waves 4-5  loader waves. They stream this CU's share of every layer's weights, plus the
+//              first 32 prefix keys/values of its attention chunk, HBM -> LDS ring with
+//              global_load_lds_dwordx4, free-running ahead of the compute waves.
 //
 // Work decomposition (XCD-aware; XCD g = blockIdx % 8, rank r = blockIdx / 8 in 0..31):
-//   XCD g owns query head g (attention), the MLP columns f in [512g, 512g+512) and the
-//   K-windows g of the O and down projections. Everything a head/F-slice needs stays inside
-//   the XCD's L2; only the O and down partial sums cross XCDs. Per layer:
-//     N1  [XCD]  QKV  [XCD]  ATT  [XCD]  COMB  [XCD]  O  [GRID]  N2  [XCD]  GU  [XCD]  DN  [GRID]
+//   XCD g owns query head g, the MLP columns f in [512g, 512g+512) and the K-windows g of the
+//   O and down projections. Per layer (sync after each stage in brackets):
+//     N1 [X] QKV [X] ATT [X] COMB [X] O {exchange} N2 [X] GU [X] DN {exchange}
+//   [X] = XCD barrier: every compute wave of the XCD stores its epoch to its own flag slot and
+//         polls the XCD's 128 slots (one 16-byte load per lane).
+//   {exchange} = the O / down partial sums are the only data crossing XCDs. Producers store
+//         them with the exchange parity in the lowest mantissa bit of every fp32 value; the
+//         consumers (N1 / N2 / final norm) poll the data itself until every value carries the
+//         current parity, so no grid-wide barrier exists anywhere.
 //   (the reference runs 9 grid-wide barriers per layer: src/pi05/mk6.cu:301-497).
-//   N1/N2/FINAL: rank r owns tokens r and r+32 of its XCD: combine the 8 XCD partials, gated
-//        residual, adaRMS -> bf16 operand. The residual x and x_t live in that CU's LDS.
+//   N1/N2/FINAL: waves 0/1 of rank r own tokens r / r+32: sum the 8 XCD partials, gated
+//        residual (the residual x and x_t live in LDS), adaRMS -> bf16 operand (or the final
+//        action projection and Euler update).
 //   QKV: 768 rows per XCD (q rows of head g + all k and v rows), 24 rows per CU, RoPE epilogue.
 //   ATT: head g, keys split into 32 chunks (one per rank); MFMA S^T = K Q^T, online softmax,
-//        O^T = V^T P^T; partial (O, m, l) per chunk.
+//        O^T = V^T P^T; normalised partial O (bf16) with (m, l) per chunk.
 //   COMB: flash-decoding combine of the 32 chunk partials -> attn_g (bf16).
-//   O:   W_o[32r..32r+32, 256g..256g+256) x attn_g -> partial o_g (sc1, cross-XCD).
+//   O:   W_o[32r..32r+32, 256g..256g+256) x attn_g -> partial o_g.
 //   GU:  32 interleaved gate/up rows per CU -> gelu_tanh(g)*u -> h_g (bf16, XCD-private).
-//   DN:  W_d[32r..32r+32, 512g..512g+512) x h_g -> partial z_g (sc1, cross-XCD).
-// GEMMs: v_mfma_f32_16x16x32_bf16 with weight rows as the A operand (16 rows x 32 k per
-// fragment, one 16-byte load per lane) and tokens as B; the 4 waves split K and reduce in LDS.
-// Weight fragments of the next GEMM stage are issued after a workgroup publishes its barrier
-// epoch and before it waits, so HBM streaming overlaps the barrier.
+//   DN:  W_d[32r..32r+32, 512g..512g+512) x h_g -> partial z_g.
+// GEMMs: v_mfma_f32_16x16x32_bf16, weight rows as the A operand (16 rows x 32 k per 1 KB
+// fragment, read from the LDS ring) and the wave's 16 tokens as B (16-byte sc1 loads from the
+// XCD's L2, all issued before the first MFMA).
 #include "fa_device.h"
 #include "../../include/flashact_mi355x.h"
 #include "fa_host.h"
@@ -28,24 +39,31 @@ namespace fa {
 namespace pi05 {
 
 constexpr int D = 1024, HD = 256, AD = 32;
-constexpr int NX = 8, NR = 32, NWG = 256, NTH = 256, TP = 64;
-constexpr int NCH = 32;  // attention key chunks per head (= ranks)
-constexpr uint32_t LDS_BYTES = 96 * 1024;  // > 80 KB forces one workgroup per CU
-constexpr uint32_t OOB = 0x80000000u;      // buffer offset past every resource: loads return 0
+constexpr int NX = 8, NR = 32, NWG = 256, TP = 64;
+constexpr int NCW = 4, NLW = 2, NTH = 64 * (NCW + NLW);  // compute waves, loader waves
+constexpr int NCH = 32;                                 // attention key chunks per head
+constexpr int RING = 9, PAGE = 16384, PPL = 13;         // ring pages, page bytes, pages per layer
+constexpr int PG_QKV = 0, PG_K = 4, PG_V = 5, PG_O = 6, PG_GU = 7, PG_DN = 11;
+constexpr int MAXF = 7;                                 // pages in flight per loader wave
+constexpr uint32_t OOB = 0x80000000u;                   // buffer offset past every resource
 
 // workspace layout (bytes)
-constexpr uint32_t OFF_CTRL = 0;          // u64 seq, u32 err
-constexpr uint32_t OFF_XFLAG = 256;       // [8][32] u64
-constexpr uint32_t OFF_GFLAG = 2304;      // [8] u64
-constexpr uint32_t OFF_XN = 4096;                                   // [8][64][1024] bf16
+constexpr uint32_t OFF_CTRL = 0;     // u64 launch sequence, u32 error bits, u32 exchange parity base
+constexpr uint32_t OFF_XFLAG = 1024; // [8 XCD][32 rank][4 wave] u64 epochs
+constexpr uint32_t OFF_XN = 16384;                                  // [8][64][1024] bf16
 constexpr uint32_t OFF_Q = OFF_XN + NX * TP * D * 2;                // [8][64][256] bf16
-constexpr uint32_t OFF_ATTP = OFF_Q + NX * TP * HD * 2;             // [8][32][64][256] f32
-constexpr uint32_t OFF_ATTML = OFF_ATTP + NX * NCH * TP * HD * 4;   // [8][32][64][2] f32
+constexpr uint32_t OFF_ATTP = OFF_Q + NX * TP * HD * 2;             // [8][32][64][256] bf16
+constexpr uint32_t OFF_ATTML = OFF_ATTP + NX * NCH * TP * HD * 2;   // [8][32][64][2] f32
 constexpr uint32_t OFF_ATTN = OFF_ATTML + NX * NCH * TP * 2 * 4;    // [8][64][256] bf16
 constexpr uint32_t OFF_H = OFF_ATTN + NX * TP * HD * 2;             // [8][64][512] bf16
-constexpr uint32_t OFF_OPART = OFF_H + NX * TP * 512 * 2;           // [8][64][1024] f32
-constexpr uint32_t OFF_ZPART = OFF_OPART + NX * TP * D * 4;         // [8][64][1024] f32
-constexpr uint32_t WS_BYTES = OFF_ZPART + NX * TP * D * 4;
+constexpr uint32_t OFF_XP = OFF_H + NX * TP * 512 * 2;              // [2][8][64][1024] f32
+constexpr uint32_t WS_BYTES = OFF_XP + 2 * NX * TP * D * 4;
+
+// LDS layout (bytes)
+constexpr uint32_t L_CTL = RING * PAGE;        // u32 ready[2], consumed[4], abort
+constexpr uint32_t L_XRES = L_CTL + 64;        // f32 [2][1024] residual stream of tokens r, r+32
+constexpr uint32_t L_XT = L_XRES + 2 * D * 4;  // f32 [2][32] x_t of tokens r, r+32
+constexpr uint32_t LDS_BYTES = L_XT + 2 * AD * 4;
 
 struct Params {
   const bf16* w1;
@@ -64,214 +82,434 @@ struct Params {
   bf16* vtcache;
   float* x_t;
   unsigned long long* stage_cycles;
+  unsigned long long* trace;
   unsigned char* ws;
-  int NL, Lp, Lmax, S, Tv, xt_rows;
+  int NL, Lp, Lmax, S, Tv, xt_rows, trace_layer;
 };
-
-// LDS map (floats)
-constexpr int L_XRES = 0;                 // [2][1024] residual stream of my two tokens
-constexpr int L_XT = L_XRES + 2 * D;      // [2][32]   x_t of my two tokens
-constexpr int L_WSUM = L_XT + 2 * AD;     // [16]      cross-wave partial sums
-constexpr int L_CW = L_WSUM + 16;         // [2][32]   combine weights
-constexpr int L_HFIN = L_CW + 64;         // [2][1024] final-norm output
-constexpr int L_RED = L_HFIN + 2 * D;     // [4 waves][8 frags][64 lanes] f32x4 (32 KB)
 
 struct Ctx {
-  int g, r, tid, lane, wave, lr, lq;
-  rsrc_t ws;      // whole workspace
-  rsrc_t kc, vc;  // caches
-  float* lds;
-  f32x4* red;
+  int g, r, wave, lane, lr, lq;
+  int kb0;              // first key of this rank's attention chunk
+  rsrc_t ws, kc, vc, rc, rs;
+  unsigned char* lds;
+  uint32_t lds_addr;    // LDS address of lds (for m0)
+  unsigned* err;
+  uint64_t e;           // epoch of this wave's latest XCD barrier
+  unsigned long long* tr;  // this wave's 32 trace slots for the traced layer, else null
 };
 
-__device__ __forceinline__ void mark(const Params& p, const Ctx& c, int idx, uint64_t& t0) {
-  if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x == 0) {
-    uint64_t now = __builtin_amdgcn_s_memrealtime();
-    p.stage_cycles[idx] += now - t0;  // slots 0-8: stage work, 9: XCD waits, 10: grid waits
-    t0 = now;
-  }
+__device__ __forceinline__ void stamp(const Ctx& c, int i) {
+  if (c.tr && c.lane == 0) c.tr[i] = __builtin_amdgcn_s_memrealtime();
 }
 
-// ---------------------------------------------------------------- GEMM core
-// acc[rt][tt] = sum over this wave's K range of W[rows rt*16+lr][k] * X[token tt*16+lr][k].
-// wf: weight fragments already in registers. X fragments are read here with sc1 loads from
-// the XCD-private operand at byte offset xoff (row t=lr, k = wave start + 8*lq), rows xrow bytes.
-template <int RT, int KS>
-__device__ __forceinline__ void gemm_core(f32x4 (&acc)[RT][4], const u32x4 (&wf)[RT][KS], const Ctx& c, uint32_t xoff,
-                                          uint32_t xrow, int Tv) {
-  u32x4 xf[4][KS];
-#pragma unroll
-  for (int tt = 0; tt < 4; tt++) {
-    const uint32_t base = tt * 16 + c.lr < Tv ? xoff + tt * 16 * xrow : OOB;
-#pragma unroll
-    for (int ks = 0; ks < KS; ks++) xf[tt][ks] = ldb128<kCpSc1>(c.ws, base + ks * 64);
-  }
-#pragma unroll
-  for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-    for (int tt = 0; tt < 4; tt++) acc[rt][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ks = 0; ks < KS; ks++)
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-      for (int tt = 0; tt < 4; tt++) acc[rt][tt] = mfma16(wf[rt][ks], xf[tt][ks], acc[rt][tt]);
+__device__ __forceinline__ volatile unsigned* lctl(const Ctx& c) {
+  return reinterpret_cast<volatile unsigned*>(c.lds + L_CTL);
 }
 
-// Cross-wave K reduction: after this, reduce_get(rt) returns the full sum of fragment
-// (rt, token tile = this wave).
-template <int RT>
-__device__ __forceinline__ void reduce_put(const Ctx& c, const f32x4 (&acc)[RT][4]) {
-#pragma unroll
-  for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-    for (int tt = 0; tt < 4; tt++) c.red[((c.wave * RT + rt) * 4 + tt) * 64 + c.lane] = acc[rt][tt];
-  __syncthreads();
-}
-template <int RT>
-__device__ __forceinline__ f32x4 reduce_get(const Ctx& c, int rt) {
-  f32x4 s = c.red[((0 * RT + rt) * 4 + c.wave) * 64 + c.lane];
-#pragma unroll
-  for (int w = 1; w < 4; w++) s += c.red[((w * RT + rt) * 4 + c.wave) * 64 + c.lane];
-  return s;
-}
-
-// ---------------------------------------------------------------- norm stages
-// MODE 0: x = embed(x_t) (layer 0).  MODE 1: x += gate * sum_g part_g.  MODE 2: as 1, final norm.
-// Writes xres (LDS) and xn_g (bf16) or, for MODE 2, the fp32 normalised rows to LDS.
-template <int MODE>
-__device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, uint32_t part_off, const float* gate,
-                                           const float* scale, const float* shift) {
-  float* xres = c.lds + L_XRES;
-  float* xt = c.lds + L_XT;
-  float* wsum = c.lds + L_WSUM;
-  const int d0 = c.tid * 4;
-  f32x4 xv[2];
-  float ss[2];
-  u32x4 part[2][NX];
-  if (MODE != 0) {
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int t = c.r + 32 * j;
-#pragma unroll
-      for (int gg = 0; gg < NX; gg++)
-        part[j][gg] = ldb128<kCpSc1>(c.ws, t < p.Tv ? part_off + ((gg * TP + t) * D + d0) * 4 : OOB);
+// ---------------------------------------------------------------- XCD barrier (per wave)
+__device__ __forceinline__ void xcd_sync(const Params& p, Ctx& c) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have reached L2
+  c.e += 1;
+  if (c.lane == 0)
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p.ws + OFF_XFLAG) + (c.g * NR + c.r) * NCW + c.wave, c.e,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin) return;
+  const uint32_t off = OFF_XFLAG + c.g * (NR * NCW * 8) + c.lane * 16;
+  for (unsigned it = 0;; ++it) {
+    const u32x4 v = ldb128<kCpSc1>(c.ws, off);
+    const uint64_t a = ((uint64_t)v[1] << 32) | v[0];
+    const uint64_t b = ((uint64_t)v[3] << 32) | v[2];
+    if (__builtin_amdgcn_ballot_w64(!(a >= c.e && b >= c.e)) == 0) break;
+    if (it > kSpinCap) {
+      if (c.lane == 0) atomicOr(c.err, kErrSpin);
+      break;
     }
+    __builtin_amdgcn_s_sleep(2);
   }
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int t = c.r + 32 * j;
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (t < p.Tv) {
-      if (MODE == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float* w = p.w_ain + (d0 + i) * AD;
-          float a = p.b_ain[d0 + i];
-#pragma unroll 8
-          for (int k = 0; k < AD; k++) a = fmaf(w[k], xt[j * AD + k], a);
-          v[i] = a;
-        }
-      } else {
-        f32x4 sum = as_f32x4(part[j][0]);
-#pragma unroll
-        for (int gg = 1; gg < NX; gg++) sum += as_f32x4(part[j][gg]);
-        const f32x4 gt = *reinterpret_cast<const f32x4*>(gate + d0);
-        const f32x4 xo = *reinterpret_cast<const f32x4*>(xres + j * D + d0);
-        v = xo + gt * sum;
-      }
-    }
-    xv[j] = v;
-    ss[j] = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-  }
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    float s = wave_sum(ss[j]);
-    if (c.lane == 0) wsum[c.wave * 2 + j] = s;
-  }
-  __syncthreads();
-  const f32x4 sc = *reinterpret_cast<const f32x4*>(scale + d0);
-  const f32x4 sh = *reinterpret_cast<const f32x4*>(shift + d0);
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int t = c.r + 32 * j;
-    if (t >= p.Tv) continue;
-    const float tot = (wsum[0 * 2 + j] + wsum[1 * 2 + j]) + (wsum[2 * 2 + j] + wsum[3 * 2 + j]);
-    const float rr = rsqrtf(tot / (float)D + 1e-6f);
-    *reinterpret_cast<f32x4*>(xres + j * D + d0) = xv[j];
-    f32x4 h;
-#pragma unroll
-    for (int i = 0; i < 4; i++) h[i] = xv[j][i] * rr * (1.0f + sc[i]) + sh[i];
-    if (MODE == 2) {
-      *reinterpret_cast<f32x4*>(c.lds + L_HFIN + j * D + d0) = h;
-    } else {
-      u32x2 pk = {pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
-      *reinterpret_cast<u32x2*>(p.ws + OFF_XN + ((c.g * TP + t) * D + d0) * 2) = pk;
-    }
-  }
-  __syncthreads();
+  asm volatile("" ::: "memory");  // loads after the barrier stay after it
 }
 
-// action_out + Euler update of my two tokens (after stage_norm<2>)
-__device__ __forceinline__ void stage_action(const Params& p, const Ctx& c, float dt) {
-  const float* hf = c.lds + L_HFIN;
-  float* xt = c.lds + L_XT;
-#pragma unroll 1
-  for (int ai = 0; ai < 8; ai++) {
-    const int a = c.wave * 8 + ai;
-    float acc[2] = {0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int d = k * 256 + c.lane * 4;
-      const f32x4 w = *reinterpret_cast<const f32x4*>(p.w_aout + a * D + d);
-#pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const f32x4 h = *reinterpret_cast<const f32x4*>(hf + j * D + d);
-        acc[j] += w[0] * h[0] + w[1] * h[1] + w[2] * h[2] + w[3] * h[3];
-      }
+// ---------------------------------------------------------------- weight ring
+// Compute wave side: wait until both loader waves have landed page pg; release pages < upto.
+__device__ __forceinline__ void page_wait(const Ctx& c, int pg) {
+  volatile unsigned* ctl = lctl(c);
+  for (unsigned it = 0;; ++it) {
+    const unsigned r0 = ctl[0], r1 = ctl[1];
+    if ((int)min(r0, r1) > pg || ctl[6]) break;
+    if (it > kSpinCap) {
+      ctl[6] = 1u;
+      if (c.lane == 0) atomicOr(c.err, kErrSpin);
+      break;
     }
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const float v = wave_sum(acc[j]);
-      if (c.lane == 0 && c.r + 32 * j < p.Tv) xt[j * AD + a] += dt * (v + p.b_aout[a]);
-    }
+    __builtin_amdgcn_s_sleep(1);
   }
-  __syncthreads();
+  asm volatile("" ::: "memory");  // ring reads stay after the wait
+}
+__device__ __forceinline__ void page_release(const Ctx& c, int upto) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS reads have returned
+  if (c.lane == 0) lctl(c)[2 + c.wave] = (unsigned)upto;
 }
 
-// ---------------------------------------------------------------- QKV
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
+  // global_load_lds_dwordx4: lane i copies 16 bytes from g to LDS m0 + 16 i, so a fragment lands
+  // in MFMA lane order. Inline asm keeps the compiler from draining these copies at waits it
+  // inserts for other memory operations; m0 is saved and restored (the compiler reserves it).
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory");
+}
+
 __device__ __forceinline__ int qkv_row(int g, int vr) {
   return vr < 256 ? 256 * g + vr : (vr < 512 ? 2048 + (vr - 256) : 2304 + (vr - 512));
 }
 
-__device__ __forceinline__ void load_w_qkv(const Params& p, const Ctx& c, int l, u32x4 (&w)[2][8]) {
+// Pages of one layer (i = page index within the layer). Loader wave lw copies fragments
+// 8lw..8lw+7 of each page; fragment f lands at ring slot offset f*1024 in MFMA lane order.
+//   0-3 QKV  (fragment F = 16i + f: row tile F/32, k-step F%32; 24 rows, tile 1 holds 8)
+//   4   K    (F: key tile F/8, k-step F%8) of keys kb0..kb0+31 (prefix rows only)
+//   5   V^T  (F: dim tile; lane (lr, lq) holds keys kb0 + 8lq .. +8 of dim 16F + lr)
+//   6   O    (F: row tile F/8, k-step F%8) of W_o[32r.., 256g..]
+//   7-10 GU  (F = 16(i-7) + f: row tile F/32, k-step F%32)
+//   11-12 DN (F = 16(i-11) + f: row tile F/16, k-step F%16)
+// Within one wave's half page, fragment ff (0..7) of every kind sits at a fixed byte stride from
+// fragment 0, and layer l at a fixed stride from layer 0, so each lane precomputes one base
+// address per page kind. Lanes whose rows this CU does not use copy a row it does (QKV tile 1
+// lanes 8-15, keys past the prefix), so every copy runs with a full exec mask.
+struct LoaderBases {
+  const unsigned char* b[PPL];
+};
+
+__device__ __forceinline__ void loader_bases(const Params& p, const Ctx& c, int lw, LoaderBases& L) {
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++) {
-    const bool ok = rt == 0 || c.lr < 8;
-    const int row = qkv_row(c.g, 24 * c.r + rt * 16 + c.lr);
-    const bf16* base = p.w1 + ((size_t)l * 2560 + (ok ? row : 0)) * D + c.wave * 256 + c.lq * 8;
+  for (int i = 0; i < 4; i++) {
+    const int F0 = 16 * i + 8 * lw, rt = F0 >> 5, ks0 = F0 & 31;
+    const int lr = (rt == 1 && c.lr >= 8) ? c.lr - 8 : c.lr;
+    L.b[i] = reinterpret_cast<const unsigned char*>(p.w1 + (size_t)qkv_row(c.g, 24 * c.r + rt * 16 + lr) * D +
+                                                    ks0 * 32 + c.lq * 8);
+  }
+  {
+    int key = c.kb0 + 16 * lw + c.lr;
+    if (key >= p.Lp) key = 0;
+    L.b[PG_K] = reinterpret_cast<const unsigned char*>(p.kcache + (size_t)key * HD + c.lq * 8);
+    int kv = c.kb0 + 8 * c.lq;
+    if (kv + 8 > p.Lp) kv = 0;
+    L.b[PG_V] = reinterpret_cast<const unsigned char*>(p.vtcache + (size_t)(128 * lw + c.lr) * p.Lmax + kv);
+  }
+  L.b[PG_O] = reinterpret_cast<const unsigned char*>(p.wo + (size_t)(32 * c.r + 16 * lw + c.lr) * 2048 + 256 * c.g +
+                                                     c.lq * 8);
 #pragma unroll
-    for (int ks = 0; ks < 8; ks++) w[rt][ks] = ok ? ld_stream128(base + ks * 32) : u32x4{0, 0, 0, 0};
+  for (int i = PG_GU; i < PG_DN; i++) {
+    const int F0 = 16 * (i - PG_GU) + 8 * lw, rt = F0 >> 5, ks0 = F0 & 31;
+    L.b[i] = reinterpret_cast<const unsigned char*>(p.w2 + (size_t)(1024 * c.g + 32 * c.r + 16 * rt + c.lr) * D +
+                                                    ks0 * 32 + c.lq * 8);
+  }
+#pragma unroll
+  for (int i = PG_DN; i < PPL; i++)
+    L.b[i] = reinterpret_cast<const unsigned char*>(p.w3 + (size_t)(32 * c.r + 16 * (i - PG_DN) + c.lr) * 4096 +
+                                                    512 * c.g + 8 * lw * 32 + c.lq * 8);
+}
+
+#define FA_VMCNT(n) (((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+// Wait until at most 8n of this wave's copies are outstanding (copies complete in issue order).
+__device__ __forceinline__ void vm_wait_pages(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(FA_VMCNT(0)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(FA_VMCNT(8)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(FA_VMCNT(16)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(FA_VMCNT(24)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(FA_VMCNT(32)); break;
+    case 5: __builtin_amdgcn_s_waitcnt(FA_VMCNT(40)); break;
+    default: __builtin_amdgcn_s_waitcnt(FA_VMCNT(48)); break;
+  }
+  asm volatile("" ::: "memory");
+}
+
+// Loader wave main loop: pages are issued in launch order; page pg needs its ring slot free
+// (every compute wave has released page pg - RING) and fewer than MAXF pages of this wave in
+// flight. While it cannot issue, the wave completes its oldest page and publishes
+// ready[lw] = number of pages landed. Ends when every page has landed (or on abort).
+__device__ void loader_main(const Params& p, const Ctx& c, int lw) {
+  volatile unsigned* ctl = lctl(c);
+  LoaderBases L;
+  loader_bases(p, c, lw, L);
+  const int NL = p.NL;
+  const int total = p.S * NL * PPL;
+  const size_t kvl = (size_t)p.Lmax * HD * 2;  // layer stride of both caches (bytes)
+  const uint32_t vfs = 16u * p.Lmax * 2;       // V^T fragment stride: 16 dims
+  int done = 0;
+  bool ok = true;
+  // diagnostics: issue / wait / landing time of each page of the traced layer (loader wave 0)
+  unsigned long long* tr = (p.trace && lw == 0) ? p.trace + ((size_t)blockIdx.x * (NCW + 2) + NCW) * 32 : nullptr;
+  const int tpg0 = p.trace_layer * PPL;
+  auto complete_oldest = [&](int issued) {
+    if (tr && c.lane == 0 && done >= tpg0 && done < tpg0 + PPL) tr[32 + done - tpg0] = __builtin_amdgcn_s_memrealtime();
+    vm_wait_pages(issued - done - 1);
+    if (tr && c.lane == 0 && done >= tpg0 && done < tpg0 + PPL)
+      tr[2 * (done - tpg0) + 1] = __builtin_amdgcn_s_memrealtime();
+    ++done;
+    if (c.lane == 0) ctl[lw] = (unsigned)done;
+  };
+#pragma unroll 1
+  for (int li = 0; li < p.S * NL && ok; li++) {
+    const int l = li - (li / NL) * NL;
+#pragma unroll
+    for (int i = 0; i < PPL; i++) {
+      const int pg = li * PPL + i;
+      // make room for page pg
+      for (unsigned idle = 0;;) {
+        if (pg - done < MAXF) {
+          if (pg < RING) break;
+          const unsigned m = min(min(ctl[2], ctl[3]), min(ctl[4], ctl[5]));
+          if ((int)m >= pg - RING + 1) break;
+        }
+        if (done < pg) {
+          complete_oldest(pg);
+          idle = 0;
+          continue;
+        }
+        if (ctl[6] || ++idle > kSpinCap) {
+          if (!ctl[6]) {
+            ctl[6] = 1u;
+            if (c.lane == 0) atomicOr(c.err, kErrSpin);
+          }
+          ok = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (!ok) break;
+      const size_t lstride = i < PG_K ? (size_t)2560 * D * 2
+                           : i <= PG_V ? kvl
+                           : i == PG_O ? (size_t)D * 2048 * 2
+                           : i < PG_DN ? (size_t)8192 * D * 2
+                                       : (size_t)D * 4096 * 2;
+      const uint32_t fstride = i == PG_V ? vfs : 64u;
+      const unsigned char* src = L.b[i] + (size_t)l * lstride;
+      const uint32_t dst = c.lds_addr + (uint32_t)(pg % RING) * PAGE + lw * 8 * 1024;
+#pragma unroll
+      for (int ff = 0; ff < 8; ff++) dma16(src + ff * fstride, dst + ff * 1024);
+      if (tr && c.lane == 0 && pg >= tpg0 && pg < tpg0 + PPL) tr[2 * (pg - tpg0)] = __builtin_amdgcn_s_memrealtime();
+    }
+  }
+  if (ok)
+    while (done < total) complete_oldest(total);
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
+// ---------------------------------------------------------------- GEMM (one token tile)
+// acc[rt] = sum_k W[row tile rt][k] * X[token 16w+lr][k] over KS k-steps. Weight fragment
+// F = rt*KS + ks is slot F%16 of ring page pg0 + F/16. xoff = byte offset in the workspace of
+// X[token][k = 8 lq] (OOB for tokens >= Tv: the loads return zeros); k-step ks adds 64 bytes.
+template <int RT, int KS>
+__device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0, uint32_t xoff, int ts) {
+  constexpr int NPG = (RT * KS + 15) / 16;
+  u32x4 xf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ks++) xf[ks] = ldb128<kCpSc1>(c.ws, xoff + ks * 64);
+#pragma unroll
+  for (int rt = 0; rt < RT; rt++) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  page_wait(c, pg0 + NPG - 1);
+  stamp(c, ts);
+  uint32_t slot[NPG];
+#pragma unroll
+  for (int k = 0; k < NPG; k++) slot[k] = ((pg0 + k) % RING) * PAGE + c.lane * 16;
+#pragma unroll
+  for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+      const int F = rt * KS + ks;
+      const u32x4 a = *reinterpret_cast<const u32x4*>(c.lds + slot[F >> 4] + (F & 15) * 1024);
+      acc[rt] = mfma16(a, xf[ks], acc[rt]);
+    }
+  stamp(c, ts + 1);
+}
+
+// ---------------------------------------------------------------- exchange (cross-XCD)
+__device__ __forceinline__ u32x4 tag(f32x4 v, unsigned par) {
+  u32x4 u = as_u32x4(v);
+#pragma unroll
+  for (int i = 0; i < 4; i++) u[i] = (u[i] & ~1u) | par;
+  return u;
+}
+__device__ __forceinline__ unsigned mism(u32x4 v, unsigned par) {
+  return ((v[0] ^ par) | (v[1] ^ par) | (v[2] ^ par) | (v[3] ^ par)) & 1u;
+}
+
+// Reads the 8 XCD partials of token t, columns 4*lane + 256k (k < 4), from exchange buffer buf.
+// First polls one hint word per source XCD (the 16 bytes written last-in-order by rank 31) with
+// a short sleep between polls, so waiting consumers put almost no load on the fabric; then loads
+// everything once and re-reads (again with a sleep) only the 16-byte groups whose parity is
+// still stale. Correctness rests on the per-value parity check, not on the hint.
+__device__ __forceinline__ void xread(const Ctx& c, int buf, int t, unsigned par, u32x4 (&v)[NX][4], int ts) {
+  const uint32_t b0 = OFF_XP + ((buf * NX * TP + t) * D + 4 * c.lane) * 4;
+  {
+    const uint32_t hint = c.lane < NX ? OFF_XP + (((buf * NX + c.lane) * TP + t) * D + D - 4) * 4 : OOB;
+    for (unsigned it = 0;; ++it) {
+      const u32x4 h = ldb128<kCpSc1>(c.ws, hint);
+      if (__builtin_amdgcn_ballot_w64(c.lane < NX && mism(h, par)) == 0) break;
+      if ((it & 1023) == 1023 &&
+          ((__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin) || it > kSpinCap))
+        break;
+      __builtin_amdgcn_s_sleep(4);
+    }
+  }
+#pragma unroll
+  for (int gg = 0; gg < NX; gg++)
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[gg][k] = ldb128<kCpSc1>(c.ws, b0 + (gg * TP * D + 256 * k) * 4);
+  for (unsigned it = 0;; ++it) {
+    unsigned bad = 0;
+#pragma unroll
+    for (int gg = 0; gg < NX; gg++)
+#pragma unroll
+      for (int k = 0; k < 4; k++) bad |= mism(v[gg][k], par) << (gg * 4 + k);
+    if (__builtin_amdgcn_ballot_w64(bad != 0) == 0) break;
+    if ((it & 255) == 255) {
+      if ((__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin) || it > kSpinCap) {
+        if (c.lane == 0) atomicOr(c.err, kErrSpin);
+        break;
+      }
+    }
+    __builtin_amdgcn_s_sleep(4);
+#pragma unroll
+    for (int gg = 0; gg < NX; gg++)
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        if ((bad >> (gg * 4 + k)) & 1u) v[gg][k] = ldb128<kCpSc1>(c.ws, b0 + (gg * TP * D + 256 * k) * 4);
+  }
+  asm volatile("" ::: "memory");
+  stamp(c, ts);
+}
+
+// ---------------------------------------------------------------- norm stages (waves 0, 1)
+// MODE 0: x = embed(x_t) (layer 0).  MODE 1: x += gate * sum_g part_g.  MODE 2: as 1, then the
+// final norm, action projection and Euler update of x_t. Token t = r + 32*wave; lane holds
+// columns 4*lane + 256k + i (k, i < 4).
+template <int MODE>
+__device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int buf, unsigned par, const float* gate,
+                                           const float* scale, const float* shift, float dt) {
+  const int t = c.r + 32 * c.wave;
+  float* xres = reinterpret_cast<float*>(c.lds + L_XRES) + c.wave * D;
+  float* xt = reinterpret_cast<float*>(c.lds + L_XT) + c.wave * AD;
+  f32x4 sc[4], sh[4], gt[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int d = 4 * c.lane + 256 * k;
+    sc[k] = *reinterpret_cast<const f32x4*>(scale + d);
+    sh[k] = *reinterpret_cast<const f32x4*>(shift + d);
+    if (MODE != 0) gt[k] = *reinterpret_cast<const f32x4*>(gate + d);
+  }
+  f32x4 x[4];
+  if (MODE == 0) {
+    float xa[AD];
+#pragma unroll
+    for (int a = 0; a < AD; a++) xa[a] = xt[a];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int d = 4 * c.lane + 256 * k;
+      f32x4 wv[4][8];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int q = 0; q < 8; q++) wv[i][q] = *reinterpret_cast<const f32x4*>(p.w_ain + (d + i) * AD + 4 * q);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(p.b_ain + d);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float s = b[i];
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) s = fmaf(wv[i][q][e], xa[4 * q + e], s);
+        x[k][i] = s;
+      }
+    }
+  } else {
+    u32x4 v[NX][4];
+    xread(c, buf, t, par, v, buf == 0 ? 26 : 25);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      f32x4 s = as_f32x4(v[0][k]);
+#pragma unroll
+      for (int gg = 1; gg < NX; gg++) s += as_f32x4(v[gg][k]);
+      const f32x4 xo = *reinterpret_cast<const f32x4*>(xres + 4 * c.lane + 256 * k);
+      x[k] = xo + gt[k] * s;
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; k++) ss += x[k][0] * x[k][0] + x[k][1] * x[k][1] + x[k][2] * x[k][2] + x[k][3] * x[k][3];
+  const float rr = rsqrtf(wave_sum(ss) / (float)D + 1e-6f);
+  f32x4 h[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) h[k][i] = x[k][i] * rr * (1.0f + sc[k][i]) + sh[k][i];
+  }
+  if (MODE != 2) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int d = 4 * c.lane + 256 * k;
+      *reinterpret_cast<f32x4*>(xres + d) = x[k];
+      const u32x2 pk = {pack_bf16x2(h[k][0], h[k][1]), pack_bf16x2(h[k][2], h[k][3])};
+      *reinterpret_cast<u32x2*>(p.ws + OFF_XN + ((c.g * TP + t) * D + d) * 2) = pk;
+    }
+  } else {
+    // v[a] = h . W_aout[a] + b_aout[a]; x_t += dt * v   (8 outputs per batch of loads)
+#pragma unroll 1
+    for (int a0 = 0; a0 < AD; a0 += 8) {
+      f32x4 wv[8][4];
+#pragma unroll
+      for (int a = 0; a < 8; a++)
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          wv[a][k] = *reinterpret_cast<const f32x4*>(p.w_aout + (a0 + a) * D + 4 * c.lane + 256 * k);
+#pragma unroll
+      for (int a = 0; a < 8; a++) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          s += wv[a][k][0] * h[k][0] + wv[a][k][1] * h[k][1] + wv[a][k][2] * h[k][2] + wv[a][k][3] * h[k][3];
+        s = wave_sum(s);
+        if (c.lane == 0) xt[a0 + a] += dt * (s + p.b_aout[a0 + a]);
+      }
+    }
   }
 }
 
-__device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, const u32x4 (&w)[2][8]) {
-  f32x4 acc[2][4];
-  gemm_core<2, 8>(acc, w, c, OFF_XN + ((c.g * TP + c.lr) * D + c.wave * 256 + c.lq * 8) * 2, D * 2, p.Tv);
-  reduce_put<2>(c, acc);
-  const int t = c.wave * 16 + c.lr;
+// ---------------------------------------------------------------- QKV
+__device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, int pg0) {
+  const int t = 16 * c.wave + c.lr;
+  const bool tv = t < p.Tv;
+  if (16 * c.wave >= p.Tv) {
+    page_release(c, pg0 + 4);
+    return;
+  }
+  // RoPE factors of my rows, issued ahead of the GEMM
+  u32x2 cs[2], sn[2];
 #pragma unroll
   for (int rt = 0; rt < 2; rt++) {
-    const f32x4 v = reduce_get<2>(c, rt);
+    const int vr0 = 24 * c.r + rt * 16 + 4 * c.lq;
+    const uint32_t o = (tv && vr0 < 512) ? (t * 128 + ((vr0 & 255) >> 1)) * 4 : OOB;
+    cs[rt] = ldb64<kCpPlain>(c.rc, o);
+    sn[rt] = ldb64<kCpPlain>(c.rs, o);
+  }
+  f32x4 acc[2];
+  gemm_tok<2, 32>(acc, c, pg0, tv ? OFF_XN + (c.g * TP + t) * D * 2 + c.lq * 16 : OOB, 15);
+  page_release(c, pg0 + 4);
+  if (!tv) return;
+#pragma unroll
+  for (int rt = 0; rt < 2; rt++) {
     if (rt == 1 && c.lq >= 2) continue;  // rows 24r+24.. belong to the next rank
-    if (t >= p.Tv) continue;
+    const f32x4 v = acc[rt];
     const int vr0 = 24 * c.r + rt * 16 + 4 * c.lq;
     if (vr0 < 512) {
       const int j = (vr0 & 255) >> 1;  // RoPE pair index within the head
-      const float* cs = p.rope_cos + t * 128 + j;
-      const float* sn = p.rope_sin + t * 128 + j;
-      const float lo0 = v[0] * cs[0] - v[1] * sn[0], hi0 = v[1] * cs[0] + v[0] * sn[0];
-      const float lo1 = v[2] * cs[1] - v[3] * sn[1], hi1 = v[3] * cs[1] + v[2] * sn[1];
+      const float c0 = as_f32(cs[rt][0]), c1 = as_f32(cs[rt][1]);
+      const float s0 = as_f32(sn[rt][0]), s1 = as_f32(sn[rt][1]);
+      const float lo0 = v[0] * c0 - v[1] * s0, hi0 = v[1] * c0 + v[0] * s0;
+      const float lo1 = v[2] * c1 - v[3] * s1, hi1 = v[3] * c1 + v[2] * s1;
       const unsigned plo = pack_bf16x2(lo0, lo1), phi = pack_bf16x2(hi0, hi1);
       if (vr0 < 256) {
         const uint32_t off = OFF_Q + ((c.g * TP + t) * HD + j) * 2;
@@ -294,72 +532,92 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
 }
 
 // ---------------------------------------------------------------- attention partials
-// Head g, keys [r*C, r*C+C): prefix keys and this step's suffix keys both come from the caches.
-// Per 32-key block every K row fragment and V^T fragment is issued before the first MFMA.
-__device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l) {
+// Head g, keys [kbeg, kend) of chunk r, tokens of this wave's tile. The first 32 keys come from
+// the LDS pages the loader prefetched when their 16-key tile is entirely prefix; other keys
+// (this step's suffix, written by this XCD, or keys beyond the first 32) use sc1 loads.
+__device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, int pgk) {
   const int Ltot = p.Lp + p.Tv;
   const int C = 32 * ((Ltot + 32 * NCH - 1) / (32 * NCH));
-  const int kbeg = c.r * C;
-  const int kend = min(kbeg + C, Ltot);
-  const int t = c.wave * 16 + c.lr;
-  const bool tok_ok = t < p.Tv;
+  const int kbeg = c.kb0, kend = min(kbeg + C, Ltot);
+  const int t = 16 * c.wave + c.lr;
+  const bool tv = t < p.Tv;
+  if (16 * c.wave >= p.Tv) {
+    page_release(c, pgk + 2);
+    return;
+  }
+  const uint32_t pbase = ((c.g * NCH + c.r) * TP + t);
+  if (kbeg >= kend) {  // empty chunk: weight 0 in the combine
+    if (tv && c.lq == 0) {
+      const f32x2 ml = {-1e30f, 0.f};
+      *reinterpret_cast<f32x2*>(p.ws + OFF_ATTML + pbase * 8) = ml;
+    }
+    page_release(c, pgk + 2);
+    return;
+  }
   const float qscale = 1.4426950408889634f / 16.0f;  // log2(e) / sqrt(256)
-
   u32x4 qf[8];
   {
-    const uint32_t qb = tok_ok ? OFF_Q + ((c.g * TP + t) * HD + c.lq * 8) * 2 : OOB;
+    const uint32_t qb = tv ? OFF_Q + (c.g * TP + t) * HD * 2 + c.lq * 16 : OOB;
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) qf[ks] = ldb128<kCpSc1>(c.ws, qb + ks * 64);
   }
+  const bool lds0 = kbeg + 16 <= p.Lp, lds1 = kbeg + 32 <= p.Lp;
+  if (lds0) page_wait(c, pgk + 1);
+  stamp(c, 23);
+  const uint32_t kslot = (pgk % RING) * PAGE, vslot = ((pgk + 1) % RING) * PAGE;
+
   float m = -1e30f, lsum = 0.f;
   f32x4 o[16];
 #pragma unroll
   for (int dt = 0; dt < 16; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   const uint32_t kl = (uint32_t)l * p.Lmax * HD * 2;  // layer base, kcache [Lmax][256]
   const uint32_t vl = (uint32_t)l * HD * p.Lmax * 2;  // layer base, vtcache [256][Lmax]
+  const uint32_t vstep = 16 * p.Lmax * 2;             // 16 dims
 #pragma unroll 1
   for (int kb = kbeg; kb < kend; kb += 32) {
-    u32x4 kf[2][8];
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-      const int key = kb + kt * 16 + c.lr;
-      const uint32_t rb = key < kend ? kl + key * HD * 2 + c.lq * 16 : OOB;
-#pragma unroll
-      for (int ks = 0; ks < 8; ks++) kf[kt][ks] = ldb128<kCpSc1>(c.kc, rb + ks * 64);
-    }
-    // V^T fragments: dim 16dt+lr, keys kg0 = kb+4lq+(0..3) and kg1 = kb+16+4lq+(0..3).
-    // The first half is issued with K; the second after the S MFMAs release the K registers.
-    const int kg0 = kb + c.lq * 4, kg1 = kg0 + 16;
-    const uint32_t vo0 = kg0 < kend ? vl + c.lr * p.Lmax * 2 + kg0 * 2 : OOB;
-    const uint32_t vo1 = kg1 < kend ? vl + c.lr * p.Lmax * 2 + kg1 * 2 : OOB;
-    const uint32_t vstep = 16 * p.Lmax * 2;  // 16 dims
+    const bool ul[2] = {kb == kbeg && lds0, kb == kbeg && lds1};
+    // V^T operand: dim 16dt+lr, keys kg[h] = kb + 16h + 4lq + (0..3)
     u32x2 vf[16][2];
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++) {
-      vf[dt][0] = ldb64<kCpSc1>(c.vc, vo0 + (vo0 == OOB ? 0 : dt * vstep));
-      vf[dt][1] = ldb64<kCpSc1>(c.vc, vo1 + (vo1 == OOB ? 0 : dt * vstep));
-    }
-    // zero V elements of keys >= kend inside a partially valid 4-key group
-    unsigned vm[2][2];
+    const int kg0 = kb + c.lq * 4;
 #pragma unroll
     for (int h2 = 0; h2 < 2; h2++) {
-      const int nv = min(max(kend - (h2 ? kg1 : kg0), 0), 4);
+      const int kg = kg0 + 16 * h2;
+      if (ul[h2]) {
+        const int o8 = 16 * h2 + 4 * c.lq;  // key offset within the 32-key block
+        const uint32_t a = vslot + (c.lr + 16 * (o8 >> 3)) * 16 + (o8 & 7) * 2;
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) vf[dt][h2] = *reinterpret_cast<const u32x2*>(c.lds + a + dt * 1024);
+      } else {
+        const uint32_t vo = kg < kend ? vl + c.lr * p.Lmax * 2 + kg * 2 : OOB;
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) vf[dt][h2] = ldb64<kCpSc1>(c.vc, vo + dt * vstep);
+      }
+    }
+    unsigned vm[2][2];  // zero V elements of keys >= kend inside a partially valid 4-key group
+#pragma unroll
+    for (int h2 = 0; h2 < 2; h2++) {
+      const int nv = min(max(kend - (kg0 + 16 * h2), 0), 4);
       vm[h2][0] = nv >= 2 ? 0xffffffffu : (nv == 1 ? 0xffffu : 0u);
       vm[h2][1] = nv >= 4 ? 0xffffffffu : (nv == 3 ? 0xffffu : 0u);
     }
     f32x4 s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
+      u32x4 kf[8];
+      if (ul[kt]) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+          kf[ks] = *reinterpret_cast<const u32x4*>(c.lds + kslot + (kt * 8 + ks) * 1024 + c.lane * 16);
+      } else {
+        const int key = kb + kt * 16 + c.lr;
+        const uint32_t rb = key < kend ? kl + key * HD * 2 + c.lq * 16 : OOB;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) kf[ks] = ldb128<kCpSc1>(c.kc, rb + ks * 64);
+      }
       f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 8; ks++) a = mfma16(kf[kt][ks], qf[ks], a);
+      for (int ks = 0; ks < 8; ks++) a = mfma16(kf[ks], qf[ks], a);
       s[kt] = a;
-    }
-#pragma unroll
-    for (int dt = 8; dt < 16; dt++) {
-      vf[dt][0] = ldb64<kCpSc1>(c.vc, vo0 + (vo0 == OOB ? 0 : dt * vstep));
-      vf[dt][1] = ldb64<kCpSc1>(c.vc, vo1 + (vo1 == OOB ? 0 : dt * vstep));
     }
     // lane holds S^T[key kb + 16kt + 4lq + i][token lr]
     float bmax = -1e30f;
@@ -392,7 +650,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l) 
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);
     lsum = lsum * alpha + psum;
-    // B operand P^T: k-slot 8lq+i <-> key kg0+i (i<4), kg1+(i-4) (i>=4)
+    // B operand P^T: k-slot 8lq+i <-> key kg0+i (i<4), kg0+16+(i-4) (i>=4); V^T uses the same order
     const u32x4 pb = {pk[0], pk[1], pk[2], pk[3]};
 #pragma unroll
     for (int dt = 0; dt < 16; dt++) {
@@ -401,263 +659,234 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l) 
       o[dt] = mfma16(va, pb, o[dt] * alpha);
     }
   }
-  // lane holds O^T[dim 16dt + 4lq + i][token lr]
-  if (tok_ok) {
-    const uint32_t base = OFF_ATTP + (((c.g * NCH + c.r) * TP + t) * HD + c.lq * 4) * 4;
+  stamp(c, 24);
+  page_release(c, pgk + 2);
+  // lane holds O^T[dim 16dt + 4lq + i][token lr]: store O / l (bf16) and (m, l)
+  if (tv) {
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    const uint32_t base = OFF_ATTP + (pbase * HD + c.lq * 4) * 2;
 #pragma unroll
-    for (int dt = 0; dt < 16; dt++) *reinterpret_cast<f32x4*>(p.ws + base + dt * 64) = o[dt];
+    for (int dt = 0; dt < 16; dt++) {
+      const u32x2 pk = {pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv), pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv)};
+      *reinterpret_cast<u32x2*>(p.ws + base + dt * 32) = pk;
+    }
     if (c.lq == 0) {
-      f32x2 ml = {m, lsum};
-      *reinterpret_cast<f32x2*>(p.ws + OFF_ATTML + (((c.g * NCH + c.r) * TP + t) * 2) * 4) = ml;
+      const f32x2 ml = {m, lsum};
+      *reinterpret_cast<f32x2*>(p.ws + OFF_ATTML + pbase * 8) = ml;
     }
   }
 }
 
 // ---------------------------------------------------------------- combine
-// attn_g[t] = sum_ch 2^(m_ch - M) O_ch[t] / sum_ch 2^(m_ch - M) l_ch for my tokens r, r+32.
+// attn_g[t] = sum_ch w_ch O_ch[t] with w_ch = l_ch 2^(m_ch - M) / sum l 2^(m - M). Wave w handles
+// token r + 32(w/2), dims 128(w%2) + 2 lane, +1.
 __device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c) {
-  float* cw = c.lds + L_CW;
-  float* red2 = reinterpret_cast<float*>(c.red);  // [4 chunk groups][2 tokens][256]
-  if (c.tid < 64) {
-    const int j = c.tid >> 5, ch = c.tid & 31;
-    const int t = c.r + 32 * j;
-    const u32x2 v = ldb64<kCpSc1>(c.ws, t < p.Tv ? OFF_ATTML + (((c.g * NCH + ch) * TP + t) * 2) * 4 : OOB);
-    const float mc = t < p.Tv ? as_f32(v[0]) : -1e30f;
-    const float lc = as_f32(v[1]);
-    float M = mc;
+  const int t = c.r + 32 * (c.wave >> 1);
+  if (t >= p.Tv) return;
+  const int d0 = 128 * (c.wave & 1) + 2 * c.lane;
+  unsigned v[NCH];
 #pragma unroll
-    for (int o = 16; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    const float wgt = exp2f(mc - M);
-    float L = wgt * lc;
+  for (int ch = 0; ch < NCH; ch++)
+    v[ch] = __builtin_amdgcn_raw_buffer_load_b32(c.ws, OFF_ATTP + (((c.g * NCH + ch) * TP + t) * HD + d0) * 2, 0,
+                                                 kCpSc1);
+  const u32x2 ml = ldb64<kCpSc1>(c.ws, c.lane < NCH ? OFF_ATTML + ((c.g * NCH + c.lane) * TP + t) * 8 : OOB);
+  const float mc = c.lane < NCH ? as_f32(ml[0]) : -1e30f;
+  const float lc = c.lane < NCH ? as_f32(ml[1]) : 0.f;
+  const float M = wave_max(mc);
+  const float w = lc * exp2f(mc - M);
+  const float wgt = w / wave_sum(w);
+  float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-    for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
-    cw[j * 32 + ch] = (t < p.Tv) ? wgt / L : 0.f;
-  }
-  const int q = c.tid & 63, cg = c.tid >> 6;  // dims 4q..4q+3, chunks 8cg..8cg+7
-  u32x4 buf[2][8];
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int t = c.r + 32 * j;
-#pragma unroll
-    for (int k = 0; k < 8; k++)
-      buf[j][k] = ldb128<kCpSc1>(
-          c.ws, t < p.Tv ? OFF_ATTP + (((c.g * NCH + cg * 8 + k) * TP + t) * HD + 4 * q) * 4 : OOB);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < 8; k++) acc += cw[j * 32 + cg * 8 + k] * as_f32x4(buf[j][k]);
-    *reinterpret_cast<f32x4*>(red2 + (cg * 2 + j) * HD + 4 * q) = acc;
-  }
-  __syncthreads();
-  if (c.tid < 128) {
-    const int j = c.tid >> 6, t = c.r + 32 * j;
-    if (t < p.Tv) {
-      f32x4 a = *reinterpret_cast<const f32x4*>(red2 + (0 * 2 + j) * HD + 4 * q);
-#pragma unroll
-      for (int g2 = 1; g2 < 4; g2++) a += *reinterpret_cast<const f32x4*>(red2 + (g2 * 2 + j) * HD + 4 * q);
-      const u32x2 pk = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
-      *reinterpret_cast<u32x2*>(p.ws + OFF_ATTN + ((c.g * TP + t) * HD + 4 * q) * 2) = pk;
+  for (int ch = 0; ch < NCH; ch++) {
+    const float wc = as_f32(__builtin_amdgcn_readlane(as_u32(wgt), ch));
+    if (wc != 0.f) {  // empty chunks hold no partial
+      a0 = fmaf(wc, bf_lo(v[ch]), a0);
+      a1 = fmaf(wc, bf_hi(v[ch]), a1);
     }
   }
+  *reinterpret_cast<unsigned*>(p.ws + OFF_ATTN + ((c.g * TP + t) * HD + d0) * 2) = pack_bf16x2(a0, a1);
 }
 
 // ---------------------------------------------------------------- O projection (K-window g)
-__device__ __forceinline__ void load_w_o(const Params& p, const Ctx& c, int l, u32x4 (&w)[2][2]) {
+// Writes all 16 token slots of the tile (zeros past Tv) so every exchange slot carries the
+// current parity.
+__device__ __forceinline__ void stage_oproj(const Params& p, const Ctx& c, int pg, unsigned par) {
+  const int t = 16 * c.wave + c.lr;
+  const bool tv = t < p.Tv;
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  if (16 * c.wave < p.Tv) gemm_tok<2, 8>(acc, c, pg, tv ? OFF_ATTN + (c.g * TP + t) * HD * 2 + c.lq * 16 : OOB, 17);
+  page_release(c, pg + 1);
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++) {
-    const bf16* base = p.wo + ((size_t)l * D + 32 * c.r + rt * 16 + c.lr) * 2048 + 256 * c.g + c.wave * 64 + c.lq * 8;
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) w[rt][ks] = ld_stream128(base + ks * 32);
-  }
-}
-
-__device__ __forceinline__ void stage_oproj(const Params& p, const Ctx& c, const u32x4 (&w)[2][2]) {
-  f32x4 acc[2][4];
-  gemm_core<2, 2>(acc, w, c, OFF_ATTN + ((c.g * TP + c.lr) * HD + c.wave * 64 + c.lq * 8) * 2, HD * 2, p.Tv);
-  reduce_put<2>(c, acc);
-  const int t = c.wave * 16 + c.lr;
-#pragma unroll
-  for (int rt = 0; rt < 2; rt++) {
-    const f32x4 v = reduce_get<2>(c, rt);
-    if (t < p.Tv)
-      stb128<kCpSc1>(c.ws, OFF_OPART + ((c.g * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 4,
-                     as_u32x4(v));
-  }
+  for (int rt = 0; rt < 2; rt++)
+    stb128<kCpSc1>(c.ws, OFF_XP + (((0 * NX + c.g) * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 4,
+                   tag(tv ? acc[rt] : f32x4{0.f, 0.f, 0.f, 0.f}, par));
 }
 
 // ---------------------------------------------------------------- gate/up (F-slice g)
-__device__ __forceinline__ void load_w_gu(const Params& p, const Ctx& c, int l, u32x4 (&w)[2][8]) {
-#pragma unroll
-  for (int rt = 0; rt < 2; rt++) {
-    const bf16* base = p.w2 + ((size_t)l * 8192 + 1024 * c.g + 32 * c.r + rt * 16 + c.lr) * D + c.wave * 256 + c.lq * 8;
-#pragma unroll
-    for (int ks = 0; ks < 8; ks++) w[rt][ks] = ld_stream128(base + ks * 32);
+__device__ __forceinline__ void stage_gu(const Params& p, const Ctx& c, int pg0) {
+  const int t = 16 * c.wave + c.lr;
+  const bool tv = t < p.Tv;
+  if (16 * c.wave >= p.Tv) {
+    page_release(c, pg0 + 4);
+    return;
   }
-}
-
-__device__ __forceinline__ void stage_gu(const Params& p, const Ctx& c, const u32x4 (&w)[2][8]) {
-  f32x4 acc[2][4];
-  gemm_core<2, 8>(acc, w, c, OFF_XN + ((c.g * TP + c.lr) * D + c.wave * 256 + c.lq * 8) * 2, D * 2, p.Tv);
-  reduce_put<2>(c, acc);
-  const int t = c.wave * 16 + c.lr;
+  f32x4 acc[2];
+  gemm_tok<2, 32>(acc, c, pg0, tv ? OFF_XN + (c.g * TP + t) * D * 2 + c.lq * 16 : OOB, 19);
+  page_release(c, pg0 + 4);
+  if (!tv) return;
 #pragma unroll
   for (int rt = 0; rt < 2; rt++) {
-    const f32x4 v = reduce_get<2>(c, rt);
-    if (t >= p.Tv) continue;
-    const int f0 = 16 * c.r + 8 * rt + 2 * c.lq;  // local MLP column of rows (gate, up) pairs
+    const f32x4 v = acc[rt];
+    const int f0 = 16 * c.r + 8 * rt + 2 * c.lq;  // local MLP column of the (gate, up) row pairs
     *reinterpret_cast<unsigned*>(p.ws + OFF_H + ((c.g * TP + t) * 512 + f0) * 2) =
         pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]);
   }
 }
 
 // ---------------------------------------------------------------- down (K-window g)
-__device__ __forceinline__ void load_w_dn(const Params& p, const Ctx& c, int l, u32x4 (&w)[2][4]) {
+__device__ __forceinline__ void stage_dn(const Params& p, const Ctx& c, int pg0, unsigned par) {
+  const int t = 16 * c.wave + c.lr;
+  const bool tv = t < p.Tv;
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  if (16 * c.wave < p.Tv) gemm_tok<2, 16>(acc, c, pg0, tv ? OFF_H + (c.g * TP + t) * 512 * 2 + c.lq * 16 : OOB, 21);
+  page_release(c, pg0 + 2);
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++) {
-    const bf16* base = p.w3 + ((size_t)l * D + 32 * c.r + rt * 16 + c.lr) * 4096 + 512 * c.g + c.wave * 128 + c.lq * 8;
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) w[rt][ks] = ld_stream128(base + ks * 32);
-  }
+  for (int rt = 0; rt < 2; rt++)
+    stb128<kCpSc1>(c.ws, OFF_XP + (((1 * NX + c.g) * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 4,
+                   tag(tv ? acc[rt] : f32x4{0.f, 0.f, 0.f, 0.f}, par));
 }
 
-__device__ __forceinline__ void stage_dn(const Params& p, const Ctx& c, const u32x4 (&w)[2][4]) {
-  f32x4 acc[2][4];
-  gemm_core<2, 4>(acc, w, c, OFF_H + ((c.g * TP + c.lr) * 512 + c.wave * 128 + c.lq * 8) * 2, 512 * 2, p.Tv);
-  reduce_put<2>(c, acc);
-  const int t = c.wave * 16 + c.lr;
-#pragma unroll
-  for (int rt = 0; rt < 2; rt++) {
-    const f32x4 v = reduce_get<2>(c, rt);
-    if (t < p.Tv)
-      stb128<kCpSc1>(c.ws, OFF_ZPART + ((c.g * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 4,
-                     as_u32x4(v));
+// ---------------------------------------------------------------- instrumentation
+__device__ __forceinline__ void mark(const Params& p, const Ctx& c, int idx, uint64_t& t0) {
+  if (p.stage_cycles && blockIdx.x == 0 && c.wave == 0 && c.lane == 0) {
+    const uint64_t now = __builtin_amdgcn_s_memrealtime();
+    p.stage_cycles[idx] += now - t0;  // 0-7 stages N1 QKV ATT COMB O N2 GU DN, 8 final, 9 XCD waits
+    t0 = now;
   }
 }
 
 // ---------------------------------------------------------------- kernel
 __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
-  extern __shared__ __attribute__((aligned(16))) float lds[];
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   Ctx c;
-  c.tid = threadIdx.x;
-  c.lane = c.tid & 63;
-  c.wave = c.tid >> 6;
+  const int tid = threadIdx.x;
+  c.lane = tid & 63;
+  c.wave = tid >> 6;
   c.lr = c.lane & 15;
   c.lq = c.lane >> 4;
   c.g = blockIdx.x & 7;
   c.r = blockIdx.x >> 3;
+  {
+    const int Ltot = p.Lp + p.Tv;
+    c.kb0 = c.r * 32 * ((Ltot + 32 * NCH - 1) / (32 * NCH));
+  }
   c.ws = make_rsrc(p.ws, WS_BYTES);
   c.kc = make_rsrc(p.kcache, (uint32_t)((size_t)p.NL * p.Lmax * HD * 2));
   c.vc = make_rsrc(p.vtcache, (uint32_t)((size_t)p.NL * p.Lmax * HD * 2));
-  c.lds = lds;
-  c.red = reinterpret_cast<f32x4*>(lds + L_RED);
-
-  unsigned* err = reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 8);
-  if (c.tid == 0 && xcc_id() != (unsigned)c.g) atomicOr(err, kErrXcd);
-  Sync s;
-  s.xline = reinterpret_cast<uint64_t*>(p.ws + OFF_XFLAG) + c.g * NR;
-  s.gline = reinterpret_cast<uint64_t*>(p.ws + OFF_GFLAG);
-  s.err = err;
-  s.rank = c.r;
-  s.xcd = c.g;
-  s.nrank = NR;
-  s.nxcd = NX;
+  c.rc = make_rsrc(p.rope_cos, (uint32_t)(p.Tv * 128 * 4));
+  c.rs = make_rsrc(p.rope_sin, (uint32_t)(p.Tv * 128 * 4));
+  c.lds = lds_raw;
+  c.lds_addr = (uint32_t)(uintptr_t)lds_raw;
+  c.err = reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 8);
+  if (tid < 16) reinterpret_cast<volatile unsigned*>(lds_raw + L_CTL)[tid] = 0u;
+  if (tid == 0 && xcc_id() != (unsigned)c.g) atomicOr(c.err, kErrXcd);
   const uint64_t seq = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
-  s.e = seq << 32;
-
-  // my two tokens' x_t into LDS
-  if (c.tid < 64) {
-    const int j = c.tid >> 5, a = c.tid & 31, t = c.r + 32 * j;
-    lds[L_XT + j * AD + a] = t < p.Tv ? p.x_t[t * AD + a] : 0.f;
+  const unsigned xbase =
+      __hip_atomic_load(reinterpret_cast<const unsigned*>(p.ws + OFF_CTRL + 12), __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();  // the only workgroup barrier: LDS control words are initialised
+  if (c.wave >= NCW) {
+    loader_main(p, c, c.wave - NCW);
+    return;
   }
-  __syncthreads();
+  c.e = seq << 32;
+  c.tr = nullptr;
+  const int NL = p.NL;
+  const bool nw = c.wave < 2 && c.r + 32 * c.wave < p.Tv;  // this wave owns a token in norm stages
+  if (nw && c.lane < AD)
+    reinterpret_cast<float*>(c.lds + L_XT)[c.wave * AD + c.lane] = p.x_t[(c.r + 32 * c.wave) * AD + c.lane];
 
   const float dt = -1.0f / (float)p.S;
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  const int NL = p.NL;
 #pragma unroll 1
   for (int step = 0; step < p.S; step++) {
 #pragma unroll 1
     for (int l = 0; l < NL; l++) {
-      const float* mod_in = p.mods + ((size_t)(step * NL + l) * 2 + 0) * 3 * D;
-      const float* mod_post = p.mods + ((size_t)(step * NL + l) * 2 + 1) * 3 * D;
-      if (l == 0) {
-        stage_norm<0>(p, c, 0, nullptr, mod_in, mod_in + D);
-      } else {
-        const float* gprev = p.mods + ((size_t)(step * NL + l - 1) * 2 + 1) * 3 * D + 2 * D;
-        stage_norm<1>(p, c, OFF_ZPART, gprev, mod_in, mod_in + D);
+      // Lane indices are laundered each layer so the compiler recomputes addresses inside the
+      // loop instead of hoisting hundreds of loop-invariant offsets (which spill).
+      asm volatile("" : "+v"(c.lane), "+v"(c.lr), "+v"(c.lq));
+      const int li = step * NL + l;
+      const int pb = li * PPL;
+      const unsigned par = (1u + xbase + (unsigned)li) & 1u;
+      c.tr = (p.trace && li == p.trace_layer) ? p.trace + ((size_t)blockIdx.x * (NCW + 2) + c.wave) * 32 : nullptr;
+      const float* mod_in = p.mods + ((size_t)li * 2 + 0) * 3 * D;
+      const float* mod_post = p.mods + ((size_t)li * 2 + 1) * 3 * D;
+      stamp(c, 0);
+      if (nw) {
+        if (l == 0)
+          stage_norm<0>(p, c, 1, 0u, nullptr, mod_in, mod_in + D, 0.f);
+        else
+          stage_norm<1>(p, c, 1, par ^ 1u, mod_post - 6 * D + 2 * D, mod_in, mod_in + D, 0.f);
       }
+      stamp(c, 1);
       mark(p, c, 0, t0);
-      {
-        u32x4 w[2][8];
-        sync_arrive(s);
-        load_w_qkv(p, c, l, w);
-        sync_wait_xcd(s);
-        mark(p, c, 9, t0);
-        stage_qkv(p, c, l, w);
-      }
+      xcd_sync(p, c);
+      mark(p, c, 9, t0);
+      stamp(c, 2);
+      stage_qkv(p, c, l, pb + PG_QKV);
+      stamp(c, 3);
       mark(p, c, 1, t0);
-      sync_arrive(s);
-      sync_wait_xcd(s);
+      xcd_sync(p, c);
       mark(p, c, 9, t0);
-      stage_att(p, c, l);
+      stamp(c, 4);
+      stage_att(p, c, l, pb + PG_K);
+      stamp(c, 5);
       mark(p, c, 2, t0);
-      sync_arrive(s);
-      sync_wait_xcd(s);
+      xcd_sync(p, c);
       mark(p, c, 9, t0);
+      stamp(c, 6);
       stage_comb(p, c);
+      stamp(c, 7);
       mark(p, c, 3, t0);
-      {
-        u32x4 w[2][2];
-        sync_arrive(s);
-        load_w_o(p, c, l, w);
-        sync_wait_xcd(s);
-        mark(p, c, 9, t0);
-        stage_oproj(p, c, w);
-      }
+      xcd_sync(p, c);
+      mark(p, c, 9, t0);
+      stamp(c, 8);
+      stage_oproj(p, c, pb + PG_O, par);
+      stamp(c, 9);
       mark(p, c, 4, t0);
-      sync_arrive(s);
-      sync_wait_grid(s);
-      mark(p, c, 10, t0);
-      stage_norm<1>(p, c, OFF_OPART, mod_in + 2 * D, mod_post, mod_post + D);
+      if (nw) stage_norm<1>(p, c, 0, par, mod_in + 2 * D, mod_post, mod_post + D, 0.f);
+      stamp(c, 10);
       mark(p, c, 5, t0);
-      {
-        u32x4 w[2][8];
-        sync_arrive(s);
-        load_w_gu(p, c, l, w);
-        sync_wait_xcd(s);
-        mark(p, c, 9, t0);
-        stage_gu(p, c, w);
-      }
+      xcd_sync(p, c);
+      mark(p, c, 9, t0);
+      stamp(c, 11);
+      stage_gu(p, c, pb + PG_GU);
+      stamp(c, 12);
       mark(p, c, 6, t0);
-      {
-        u32x4 w[2][4];
-        sync_arrive(s);
-        load_w_dn(p, c, l, w);
-        sync_wait_xcd(s);
-        mark(p, c, 9, t0);
-        stage_dn(p, c, w);
-      }
+      xcd_sync(p, c);
+      mark(p, c, 9, t0);
+      stamp(c, 13);
+      stage_dn(p, c, pb + PG_DN, par);
+      stamp(c, 14);
       mark(p, c, 7, t0);
-      sync_arrive(s);
-      sync_wait_grid(s);
-      mark(p, c, 10, t0);
     }
-    const float* gl = p.mods + ((size_t)(step * NL + NL - 1) * 2 + 1) * 3 * D + 2 * D;
-    const float* mf = p.mod_final + (size_t)step * 3 * D;
-    stage_norm<2>(p, c, OFF_ZPART, gl, mf, mf + D);
-    stage_action(p, c, dt);
+    if (nw) {
+      const int li = step * NL + NL - 1;
+      const unsigned par = (1u + xbase + (unsigned)li) & 1u;
+      const float* gl = p.mods + ((size_t)li * 2 + 1) * 3 * D + 2 * D;
+      const float* mf = p.mod_final + (size_t)step * 3 * D;
+      stage_norm<2>(p, c, 1, par, gl, mf, mf + D, dt);
+    }
     mark(p, c, 8, t0);
   }
-  if (c.g == 0 && c.tid < 64) {
-    const int j = c.tid >> 5, a = c.tid & 31, t = c.r + 32 * j;
-    if (t < p.Tv) p.x_t[t * AD + a] = lds[L_XT + j * AD + a];
-  }
-  if (blockIdx.x == 0 && c.tid == 0)
+  if (c.g == 0 && nw && c.lane < AD)
+    p.x_t[(c.r + 32 * c.wave) * AD + c.lane] = reinterpret_cast<float*>(c.lds + L_XT)[c.wave * AD + c.lane];
+  if (blockIdx.x == 0 && c.wave == 0 && c.lane == 0) {
+    __hip_atomic_store(reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 12), (xbase + (unsigned)(p.S * NL)) & 1u,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(reinterpret_cast<uint64_t*>(p.ws + OFF_CTRL), seq + 1, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 __global__ void ws_zero(u32x4* p, size_t n16) {
@@ -667,7 +896,6 @@ __global__ void ws_zero(u32x4* p, size_t n16) {
 
 }  // namespace pi05
 }  // namespace fa
-
 // ================================================================= host C ABI
 using namespace fa;
 
@@ -756,6 +984,8 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
   p.vtcache = static_cast<bf16*>(a->vtcache);
   p.x_t = a->x_t;
   p.stage_cycles = a->stage_cycles;
+  p.trace = a->trace;
+  p.trace_layer = a->trace_layer;
   p.ws = static_cast<unsigned char*>(a->workspace);
   p.NL = a->num_layers;
   p.Lp = a->Lp;

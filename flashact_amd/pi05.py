@@ -168,7 +168,8 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
            w_ain, b_ain, w_aout, b_aout, kvsrc_k, kvsrc_v, srows,
            kcache, vtcache, Lp, Lmax, num_steps, Tv,
            x_t, x=None, xp=None, stage_cycles=None, xn=None, q=None, attn=None, hmlp=None, scores=None,
-           probs=None, nblocks=None, nthreads=None, *, num_layers=None, workspace_tensor=None):
+           probs=None, nblocks=None, nthreads=None, *, num_layers=None, workspace_tensor=None, trace=None,
+           trace_layer=0):
     """Runs the whole ``num_steps`` Euler loop; ``x_t`` is updated in place (the output).
 
     Same positional order as the reference ``launch``. Differences, all by design:
@@ -221,5 +222,9 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
             raise TypeError("stage_cycles must be an int64 tensor with >= 16 entries")
         a.stage_cycles = _ptr(stage_cycles)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    if trace is not None:
+        if trace.dtype != torch.int64 or trace.numel() < 256 * 6 * 32:
+            raise TypeError("trace must be an int64 tensor with >= 256*6*32 entries")
+        a.trace, a.trace_layer = _ptr(trace), int(trace_layer)
     stream = torch.cuda.current_stream(dev).cuda_stream
     _lib.check(L.fa_pi05_denoise(ctypes.byref(a), ctypes.c_void_p(stream)), "fa_pi05_denoise")

@@ -103,6 +103,12 @@ typedef struct fa_pi05_args {
   unsigned long long* stage_cycles; /* optional [16]: per-stage 100 MHz ticks, workgroup 0 */
   void* workspace;
   size_t workspace_bytes;
+  /* Diagnostics (optional): for global layer index trace_layer (= step * num_layers + layer),
+   * every compute wave writes the 100 MHz real-time clock at the start and end of each stage of
+   * that layer and at sub-stage points, and the first loader wave records when each of the
+   * layer's weight pages was issued and landed: trace [256 workgroups][6][32]. NULL disables. */
+  unsigned long long* trace;
+  int trace_layer;
 } fa_pi05_args;
 
 /* Whole S-step Euler loop as ONE cooperative launch (256 workgroups, one per CU). */

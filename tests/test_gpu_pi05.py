@@ -80,7 +80,7 @@ def test_pi05_stage_cycles(gpu):
     sc = torch.zeros(16, dtype=torch.int64, device=gpu)
     P.run_gpu(c, gpu, stage_cycles=sc)
     v = sc.cpu().numpy()
-    assert (v[:11] > 0).all() and (v[11:] == 0).all()
+    assert (v[:10] > 0).all() and (v[10:] == 0).all()
 
 
 def test_pi05_rejects_bad_shapes(gpu):

@@ -22,7 +22,9 @@
 //        residual (the residual x and x_t live in LDS), adaRMS -> bf16 operand (or the final
 //        action projection and Euler update).
 //   QKV: 768 rows per XCD (q rows of head g + all k and v rows), 24 rows per CU, RoPE epilogue.
-//   ATT: head g, keys split into 32 chunks (one per rank); MFMA S^T = K Q^T, online softmax,
+//   ATT: head g, keys split into 32 chunks (one per rank). Prefix keys of a chunk's first 32
+//        come from LDS (prefetched by the loader), this step's own keys from XCD-private copies
+//        in MFMA fragment order written by QKV. MFMA S^T = K Q^T, online softmax,
 //        O^T = V^T P^T; normalised partial O (bf16) with (m, l) per chunk.
 //   COMB: flash-decoding combine of the 32 chunk partials -> attn_g (bf16).
 //   O:   W_o[32r..32r+32, 256g..256g+256) x attn_g -> partial o_g.
@@ -55,9 +57,16 @@ constexpr uint32_t OFF_Q = OFF_XN + NX * TP * D * 2;                // [8][64][2
 constexpr uint32_t OFF_ATTP = OFF_Q + NX * TP * HD * 2;             // [8][32][64][256] bf16
 constexpr uint32_t OFF_ATTML = OFF_ATTP + NX * NCH * TP * HD * 2;   // [8][32][64][2] f32
 constexpr uint32_t OFF_ATTN = OFF_ATTML + NX * NCH * TP * 2 * 4;    // [8][64][256] bf16
-constexpr uint32_t OFF_H = OFF_ATTN + NX * TP * HD * 2;             // [8][64][512] bf16
+constexpr uint32_t OFF_H = OFF_ATTN + NX * TP * HD * 2;             // [8][32 rank][64][16] bf16
 constexpr uint32_t OFF_XP = OFF_H + NX * TP * 512 * 2;              // [2][8][64][1024] f32
-constexpr uint32_t WS_BYTES = OFF_XP + 2 * NX * TP * D * 4;
+// This step's own keys/values (the suffix) in MFMA fragment order, per 32-key block of the key
+// range: [8 XCD][3 blocks][2 key tiles][8 k-steps][64 lanes][8 bf16] and
+// [8 XCD][3 blocks][16 dim tiles][2 halves][64 lanes][4 bf16], so attention reads them with
+// contiguous 1 KB / 512 B loads.
+constexpr int NSB = 3;                                              // suffix blocks (Tv <= 64)
+constexpr uint32_t OFF_KFR = OFF_XP + 2 * NX * TP * D * 4;
+constexpr uint32_t OFF_VFR = OFF_KFR + NX * NSB * 16384;
+constexpr uint32_t WS_BYTES = OFF_VFR + NX * NSB * 16384;
 
 // LDS layout (bytes)
 constexpr uint32_t L_CTL = RING * PAGE;        // u32 ready[2], consumed[4], abort
@@ -87,12 +96,16 @@ struct Params {
   int NL, Lp, Lmax, S, Tv, xt_rows, trace_layer;
 };
 
+// Dynamic LDS of the kernel. Every LDS access goes through this array so the compiler keeps the
+// LDS address space and emits ds_* instructions (a generic pointer would turn them into flat
+// accesses that also wait on the vector-memory counter).
+extern __shared__ __attribute__((aligned(16))) unsigned char fa_lds[];
+
 struct Ctx {
   int g, r, wave, lane, lr, lq;
   int kb0;              // first key of this rank's attention chunk
   rsrc_t ws, kc, vc, rc, rs;
-  unsigned char* lds;
-  uint32_t lds_addr;    // LDS address of lds (for m0)
+  uint32_t lds_addr;    // LDS address of fa_lds (for m0)
   unsigned* err;
   uint64_t e;           // epoch of this wave's latest XCD barrier
   unsigned long long* tr;  // this wave's 32 trace slots for the traced layer, else null
@@ -102,8 +115,16 @@ __device__ __forceinline__ void stamp(const Ctx& c, int i) {
   if (c.tr && c.lane == 0) c.tr[i] = __builtin_amdgcn_s_memrealtime();
 }
 
-__device__ __forceinline__ volatile unsigned* lctl(const Ctx& c) {
-  return reinterpret_cast<volatile unsigned*>(c.lds + L_CTL);
+// LDS control words (ready[2], consumed[4], abort) shared by the loader and compute waves of a
+// workgroup: relaxed workgroup-scope atomics, which compile to plain ds_read/ds_write (a volatile
+// access would keep the generic address space and become a flat access).
+__device__ __forceinline__ unsigned ctl_ld(int i) {
+  return __hip_atomic_load(reinterpret_cast<unsigned*>(fa_lds + L_CTL) + i, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void ctl_st(int i, unsigned v) {
+  __hip_atomic_store(reinterpret_cast<unsigned*>(fa_lds + L_CTL) + i, v, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // ---------------------------------------------------------------- XCD barrier (per wave)
@@ -132,12 +153,11 @@ __device__ __forceinline__ void xcd_sync(const Params& p, Ctx& c) {
 // ---------------------------------------------------------------- weight ring
 // Compute wave side: wait until both loader waves have landed page pg; release pages < upto.
 __device__ __forceinline__ void page_wait(const Ctx& c, int pg) {
-  volatile unsigned* ctl = lctl(c);
   for (unsigned it = 0;; ++it) {
-    const unsigned r0 = ctl[0], r1 = ctl[1];
-    if ((int)min(r0, r1) > pg || ctl[6]) break;
+    const unsigned r0 = ctl_ld(0), r1 = ctl_ld(1);
+    if ((int)min(r0, r1) > pg || ctl_ld(6)) break;
     if (it > kSpinCap) {
-      ctl[6] = 1u;
+      ctl_st(6, 1u);
       if (c.lane == 0) atomicOr(c.err, kErrSpin);
       break;
     }
@@ -147,7 +167,7 @@ __device__ __forceinline__ void page_wait(const Ctx& c, int pg) {
 }
 __device__ __forceinline__ void page_release(const Ctx& c, int upto) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS reads have returned
-  if (c.lane == 0) lctl(c)[2 + c.wave] = (unsigned)upto;
+  if (c.lane == 0) ctl_st(2 + c.wave, (unsigned)upto);
 }
 
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
@@ -168,7 +188,7 @@ __device__ __forceinline__ int qkv_row(int g, int vr) {
 // Pages of one layer (i = page index within the layer). Loader wave lw copies fragments
 // 8lw..8lw+7 of each page; fragment f lands at ring slot offset f*1024 in MFMA lane order.
 //   0-3 QKV  (fragment F = 16i + f: row tile F/32, k-step F%32; 24 rows, tile 1 holds 8)
-//   4   K    (F: key tile F/8, k-step F%8) of keys kb0..kb0+31 (prefix rows only)
+//   4   K    (F: key tile F/8, k-step F%8) of keys kb0..kb0+31 (rows past the prefix: key 0)
 //   5   V^T  (F: dim tile; lane (lr, lq) holds keys kb0 + 8lq .. +8 of dim 16F + lr)
 //   6   O    (F: row tile F/8, k-step F%8) of W_o[32r.., 256g..]
 //   7-10 GU  (F = 16(i-7) + f: row tile F/32, k-step F%32)
@@ -193,8 +213,11 @@ __device__ __forceinline__ void loader_bases(const Params& p, const Ctx& c, int 
     int key = c.kb0 + 16 * lw + c.lr;
     if (key >= p.Lp) key = 0;
     L.b[PG_K] = reinterpret_cast<const unsigned char*>(p.kcache + (size_t)key * HD + c.lq * 8);
+    // An 8-key group that starts inside the prefix is copied from its own row even when it runs
+    // past Lp (it stays inside the row: Lmax >= 8 * ceil(Lp / 8)); keys >= Lp are masked by the
+    // attention stage. Groups entirely past the prefix copy keys 0..7 instead.
     int kv = c.kb0 + 8 * c.lq;
-    if (kv + 8 > p.Lp) kv = 0;
+    if (kv >= p.Lp) kv = 0;
     L.b[PG_V] = reinterpret_cast<const unsigned char*>(p.vtcache + (size_t)(128 * lw + c.lr) * p.Lmax + kv);
   }
   L.b[PG_O] = reinterpret_cast<const unsigned char*>(p.wo + (size_t)(32 * c.r + 16 * lw + c.lr) * 2048 + 256 * c.g +
@@ -231,7 +254,6 @@ __device__ __forceinline__ void vm_wait_pages(int n) {
 // flight. While it cannot issue, the wave completes its oldest page and publishes
 // ready[lw] = number of pages landed. Ends when every page has landed (or on abort).
 __device__ void loader_main(const Params& p, const Ctx& c, int lw) {
-  volatile unsigned* ctl = lctl(c);
   LoaderBases L;
   loader_bases(p, c, lw, L);
   const int NL = p.NL;
@@ -249,7 +271,7 @@ __device__ void loader_main(const Params& p, const Ctx& c, int lw) {
     if (tr && c.lane == 0 && done >= tpg0 && done < tpg0 + PPL)
       tr[2 * (done - tpg0) + 1] = __builtin_amdgcn_s_memrealtime();
     ++done;
-    if (c.lane == 0) ctl[lw] = (unsigned)done;
+    if (c.lane == 0) ctl_st(lw, (unsigned)done);
   };
 #pragma unroll 1
   for (int li = 0; li < p.S * NL && ok; li++) {
@@ -261,7 +283,7 @@ __device__ void loader_main(const Params& p, const Ctx& c, int lw) {
       for (unsigned idle = 0;;) {
         if (pg - done < MAXF) {
           if (pg < RING) break;
-          const unsigned m = min(min(ctl[2], ctl[3]), min(ctl[4], ctl[5]));
+          const unsigned m = min(min(ctl_ld(2), ctl_ld(3)), min(ctl_ld(4), ctl_ld(5)));
           if ((int)m >= pg - RING + 1) break;
         }
         if (done < pg) {
@@ -269,9 +291,9 @@ __device__ void loader_main(const Params& p, const Ctx& c, int lw) {
           idle = 0;
           continue;
         }
-        if (ctl[6] || ++idle > kSpinCap) {
-          if (!ctl[6]) {
-            ctl[6] = 1u;
+        if (ctl_ld(6) || ++idle > kSpinCap) {
+          if (!ctl_ld(6)) {
+            ctl_st(6, 1u);
             if (c.lane == 0) atomicOr(c.err, kErrSpin);
           }
           ok = false;
@@ -301,13 +323,13 @@ __device__ void loader_main(const Params& p, const Ctx& c, int lw) {
 // ---------------------------------------------------------------- GEMM (one token tile)
 // acc[rt] = sum_k W[row tile rt][k] * X[token 16w+lr][k] over KS k-steps. Weight fragment
 // F = rt*KS + ks is slot F%16 of ring page pg0 + F/16. xoff = byte offset in the workspace of
-// X[token][k = 8 lq] (OOB for tokens >= Tv: the loads return zeros); k-step ks adds 64 bytes.
-template <int RT, int KS>
+// X[token][k = 8 lq] (OOB for tokens >= Tv: the loads return zeros); k-step ks adds XSTRIDE bytes.
+template <int RT, int KS, int XSTRIDE = 64>
 __device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0, uint32_t xoff, int ts) {
   constexpr int NPG = (RT * KS + 15) / 16;
   u32x4 xf[KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ks++) xf[ks] = ldb128<kCpSc1>(c.ws, xoff + ks * 64);
+  for (int ks = 0; ks < KS; ks++) xf[ks] = ldb128<kCpSc1>(c.ws, xoff + ks * XSTRIDE);
 #pragma unroll
   for (int rt = 0; rt < RT; rt++) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
   page_wait(c, pg0 + NPG - 1);
@@ -320,7 +342,7 @@ __device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
       const int F = rt * KS + ks;
-      const u32x4 a = *reinterpret_cast<const u32x4*>(c.lds + slot[F >> 4] + (F & 15) * 1024);
+      const u32x4 a = *reinterpret_cast<const u32x4*>(fa_lds + slot[F >> 4] + (F & 15) * 1024);
       acc[rt] = mfma16(a, xf[ks], acc[rt]);
     }
   stamp(c, ts + 1);
@@ -391,8 +413,8 @@ template <int MODE>
 __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int buf, unsigned par, const float* gate,
                                            const float* scale, const float* shift, float dt) {
   const int t = c.r + 32 * c.wave;
-  float* xres = reinterpret_cast<float*>(c.lds + L_XRES) + c.wave * D;
-  float* xt = reinterpret_cast<float*>(c.lds + L_XT) + c.wave * AD;
+  float* xres = reinterpret_cast<float*>(fa_lds + L_XRES) + c.wave * D;
+  float* xt = reinterpret_cast<float*>(fa_lds + L_XT) + c.wave * AD;
   f32x4 sc[4], sh[4], gt[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
@@ -479,13 +501,10 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int bu
 }
 
 // ---------------------------------------------------------------- QKV
-__device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, int pg0) {
+__device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, int pg0, bool last) {
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
-  if (16 * c.wave >= p.Tv) {
-    page_release(c, pg0 + 4);
-    return;
-  }
+  const bool any = 16 * c.wave < p.Tv;
   // RoPE factors of my rows, issued ahead of the GEMM
   u32x2 cs[2], sn[2];
 #pragma unroll
@@ -495,46 +514,65 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
     cs[rt] = ldb64<kCpPlain>(c.rc, o);
     sn[rt] = ldb64<kCpPlain>(c.rs, o);
   }
-  f32x4 acc[2];
-  gemm_tok<2, 32>(acc, c, pg0, tv ? OFF_XN + (c.g * TP + t) * D * 2 + c.lq * 16 : OOB, 15);
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  if (any) gemm_tok<2, 32>(acc, c, pg0, tv ? OFF_XN + (c.g * TP + t) * D * 2 + c.lq * 16 : OOB, 15);
   page_release(c, pg0 + 4);
-  if (!tv) return;
 #pragma unroll
   for (int rt = 0; rt < 2; rt++) {
     if (rt == 1 && c.lq >= 2) continue;  // rows 24r+24.. belong to the next rank
     const f32x4 v = acc[rt];
     const int vr0 = 24 * c.r + rt * 16 + 4 * c.lq;
-    if (vr0 < 512) {
-      const int j = (vr0 & 255) >> 1;  // RoPE pair index within the head
-      const float c0 = as_f32(cs[rt][0]), c1 = as_f32(cs[rt][1]);
-      const float s0 = as_f32(sn[rt][0]), s1 = as_f32(sn[rt][1]);
-      const float lo0 = v[0] * c0 - v[1] * s0, hi0 = v[1] * c0 + v[0] * s0;
-      const float lo1 = v[2] * c1 - v[3] * s1, hi1 = v[3] * c1 + v[2] * s1;
-      const unsigned plo = pack_bf16x2(lo0, lo1), phi = pack_bf16x2(hi0, hi1);
-      if (vr0 < 256) {
-        const uint32_t off = OFF_Q + ((c.g * TP + t) * HD + j) * 2;
-        *reinterpret_cast<unsigned*>(p.ws + off) = plo;
-        *reinterpret_cast<unsigned*>(p.ws + off + 256) = phi;
-      } else {
-        // Suffix keys go to the caller's cache (the reference's output contract). Every XCD
-        // writes the same values and reads back its own L2 copy in the attention stage.
+    if (vr0 >= 512) {
+      if (!tv) continue;
+      const int d = vr0 - 512;
+      // value dims d..d+3 of key Lp+t into the fragment-ordered copy (lane dim%16 + 16*(key%16/4))
+      const int kp = p.Lp + t, st = (kp >> 5) - (p.Lp >> 5), j = kp & 31;
+      bf16* vf = reinterpret_cast<bf16*>(p.ws + OFF_VFR) +
+                 ((((c.g * NSB + st) * 16 + (d >> 4)) * 2 + (j >> 4)) * 64 + 16 * ((j & 15) >> 2)) * 4 + (j & 3);
+#pragma unroll
+      for (int i = 0; i < 4; i++) vf[((d & 15) + i) * 4] = (bf16)v[i];
+      if (last && c.g == (l & 7)) {
+        bf16* vr = p.vtcache + ((size_t)l * HD + d) * p.Lmax + p.Lp + t;
+#pragma unroll
+        for (int i = 0; i < 4; i++) vr[(size_t)i * p.Lmax] = (bf16)v[i];
+      }
+      continue;
+    }
+    if (!tv) continue;
+    const int j = (vr0 & 255) >> 1;  // RoPE pair index within the head
+    const float c0 = as_f32(cs[rt][0]), c1 = as_f32(cs[rt][1]);
+    const float s0 = as_f32(sn[rt][0]), s1 = as_f32(sn[rt][1]);
+    const float lo0 = v[0] * c0 - v[1] * s0, hi0 = v[1] * c0 + v[0] * s0;
+    const float lo1 = v[2] * c1 - v[3] * s1, hi1 = v[3] * c1 + v[2] * s1;
+    const unsigned plo = pack_bf16x2(lo0, lo1), phi = pack_bf16x2(hi0, hi1);
+    if (vr0 < 256) {
+      const uint32_t off = OFF_Q + ((c.g * TP + t) * HD + j) * 2;
+      *reinterpret_cast<unsigned*>(p.ws + off) = plo;
+      *reinterpret_cast<unsigned*>(p.ws + off + 256) = phi;
+    } else {
+      // Every XCD keeps its own fragment-ordered copy of this step's keys for attention. The
+      // caller's cache rows (the reference leaves the last step's suffix K/V there) are written
+      // in the last step only, by XCD l % 8.
+      const int kp = p.Lp + t, st = (kp >> 5) - (p.Lp >> 5), jk = kp & 31;
+      const uint32_t kb = OFF_KFR + (((c.g * NSB + st) * 2 + (jk >> 4)) * 8) * 1024 + (jk & 15) * 16;
+      // dims j, j+1 (lo) and j+128, j+129 (hi): k-step d/32, lane quarter (d%32)/8, element d%8
+      *reinterpret_cast<unsigned*>(p.ws + kb + (j >> 5) * 1024 + ((j & 31) >> 3) * 256 + (j & 7) * 2) = plo;
+      *reinterpret_cast<unsigned*>(p.ws + kb + ((j + 128) >> 5) * 1024 + ((j & 31) >> 3) * 256 + (j & 7) * 2) = phi;
+      if (last && c.g == (l & 7)) {
         bf16* kr = p.kcache + ((size_t)l * p.Lmax + p.Lp + t) * HD;
         *reinterpret_cast<unsigned*>(kr + j) = plo;
         *reinterpret_cast<unsigned*>(kr + j + 128) = phi;
       }
-    } else {
-      const int d = vr0 - 512;
-      bf16* vr = p.vtcache + ((size_t)l * HD + d) * p.Lmax + p.Lp + t;
-#pragma unroll
-      for (int i = 0; i < 4; i++) vr[(size_t)i * p.Lmax] = (bf16)v[i];
     }
   }
 }
 
 // ---------------------------------------------------------------- attention partials
-// Head g, keys [kbeg, kend) of chunk r, tokens of this wave's tile. The first 32 keys come from
-// the LDS pages the loader prefetched when their 16-key tile is entirely prefix; other keys
-// (this step's suffix, written by this XCD, or keys beyond the first 32) use sc1 loads.
+// Head g, keys [kbeg, kend) of chunk r (C = 32 ceil(Ltot/1024) keys), tokens of this wave's tile,
+// in 32-key blocks. Sources per key (K rows) or 4-key group (V^T columns): prefix keys of the
+// first block come from the LDS pages the loader prefetched, prefix keys of later blocks from the
+// caches, this step's keys from the XCD-private fragment-ordered copies; a 4-key group that
+// straddles Lp takes its prefix and suffix elements from both. Keys past kend: S = -inf, V = 0.
 __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, int pgk) {
   const int Ltot = p.Lp + p.Tv;
   const int C = 32 * ((Ltot + 32 * NCH - 1) / (32 * NCH));
@@ -561,8 +599,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) qf[ks] = ldb128<kCpSc1>(c.ws, qb + ks * 64);
   }
-  const bool lds0 = kbeg + 16 <= p.Lp, lds1 = kbeg + 32 <= p.Lp;
-  if (lds0) page_wait(c, pgk + 1);
+  if (kbeg < p.Lp) page_wait(c, pgk + 1);
   stamp(c, 23);
   const uint32_t kslot = (pgk % RING) * PAGE, vslot = ((pgk + 1) % RING) * PAGE;
 
@@ -575,50 +612,33 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
   const uint32_t vstep = 16 * p.Lmax * 2;             // 16 dims
 #pragma unroll 1
   for (int kb = kbeg; kb < kend; kb += 32) {
-    const bool ul[2] = {kb == kbeg && lds0, kb == kbeg && lds1};
-    // V^T operand: dim 16dt+lr, keys kg[h] = kb + 16h + 4lq + (0..3)
-    u32x2 vf[16][2];
+    const bool first = kb == kbeg;
+    const int st = (kb >> 5) - (p.Lp >> 5);  // suffix block of this 32-key block (if it has suffix keys)
     const int kg0 = kb + c.lq * 4;
-#pragma unroll
-    for (int h2 = 0; h2 < 2; h2++) {
-      const int kg = kg0 + 16 * h2;
-      if (ul[h2]) {
-        const int o8 = 16 * h2 + 4 * c.lq;  // key offset within the 32-key block
-        const uint32_t a = vslot + (c.lr + 16 * (o8 >> 3)) * 16 + (o8 & 7) * 2;
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++) vf[dt][h2] = *reinterpret_cast<const u32x2*>(c.lds + a + dt * 1024);
-      } else {
-        const uint32_t vo = kg < kend ? vl + c.lr * p.Lmax * 2 + kg * 2 : OOB;
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++) vf[dt][h2] = ldb64<kCpSc1>(c.vc, vo + dt * vstep);
-      }
-    }
-    unsigned vm[2][2];  // zero V elements of keys >= kend inside a partially valid 4-key group
-#pragma unroll
-    for (int h2 = 0; h2 < 2; h2++) {
-      const int nv = min(max(kend - (kg0 + 16 * h2), 0), 4);
-      vm[h2][0] = nv >= 2 ? 0xffffffffu : (nv == 1 ? 0xffffu : 0u);
-      vm[h2][1] = nv >= 4 ? 0xffffffffu : (nv == 3 ? 0xffffu : 0u);
-    }
     f32x4 s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
       u32x4 kf[8];
-      if (ul[kt]) {
+      const int key = kb + kt * 16 + c.lr;
+      if (key >= p.Lp) {
+        const uint32_t rb = key < kend ? OFF_KFR + (((c.g * NSB + st) * 2 + kt) * 8) * 1024 + c.lane * 16 : OOB;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) kf[ks] = ldb128<kCpSc1>(c.ws, rb + ks * 1024);
+      } else if (first) {
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
-          kf[ks] = *reinterpret_cast<const u32x4*>(c.lds + kslot + (kt * 8 + ks) * 1024 + c.lane * 16);
+          kf[ks] = *reinterpret_cast<const u32x4*>(fa_lds + kslot + (kt * 8 + ks) * 1024 + c.lane * 16);
       } else {
-        const int key = kb + kt * 16 + c.lr;
-        const uint32_t rb = key < kend ? kl + key * HD * 2 + c.lq * 16 : OOB;
+        const uint32_t rb = kl + key * HD * 2 + c.lq * 16;
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) kf[ks] = ldb128<kCpSc1>(c.kc, rb + ks * 64);
+        for (int ks = 0; ks < 8; ks++) kf[ks] = ldb128<kCpPlain>(c.kc, rb + ks * 64);
       }
       f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 8; ks++) a = mfma16(kf[ks], qf[ks], a);
       s[kt] = a;
     }
+    if (c.tr) stamp(c, first ? 29 : 30);
     // lane holds S^T[key kb + 16kt + 4lq + i][token lr]
     float bmax = -1e30f;
 #pragma unroll
@@ -652,11 +672,61 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
     lsum = lsum * alpha + psum;
     // B operand P^T: k-slot 8lq+i <-> key kg0+i (i<4), kg0+16+(i-4) (i>=4); V^T uses the same order
     const u32x4 pb = {pk[0], pk[1], pk[2], pk[3]};
+    unsigned vm[2][2];  // zero V elements of keys >= kend inside a partially valid 4-key group
+    int npre[2];        // keys of each 4-key group inside the prefix
 #pragma unroll
-    for (int dt = 0; dt < 16; dt++) {
-      const u32x4 va = {vf[dt][0][0] & vm[0][0], vf[dt][0][1] & vm[0][1], vf[dt][1][0] & vm[1][0],
-                        vf[dt][1][1] & vm[1][1]};
-      o[dt] = mfma16(va, pb, o[dt] * alpha);
+    for (int h2 = 0; h2 < 2; h2++) {
+      const int nv = min(max(kend - (kg0 + 16 * h2), 0), 4);
+      vm[h2][0] = nv >= 2 ? 0xffffffffu : (nv == 1 ? 0xffffu : 0u);
+      vm[h2][1] = nv >= 4 ? 0xffffffffu : (nv == 3 ? 0xffffu : 0u);
+      npre[h2] = min(max(p.Lp - (kg0 + 16 * h2), 0), 4);
+    }
+    // V^T operand (dim 16dt+lr, keys kg0 + 16h + (0..3)) in two halves of 8 dim tiles
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+      __builtin_amdgcn_sched_barrier(0);
+      u32x2 vf[8][2];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; h2++) {
+        const int kg = kg0 + 16 * h2;
+        if (npre[h2] > 0) {  // prefix elements: LDS page (first block) or the cache
+          if (first) {
+            const int o8 = 16 * h2 + 4 * c.lq;  // key offset within the 32-key block
+            const uint32_t ad = vslot + (c.lr + 16 * (o8 >> 3)) * 16 + (o8 & 7) * 2 + half * 8 * 1024;
+#pragma unroll
+            for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = *reinterpret_cast<const u32x2*>(fa_lds + ad + d8 * 1024);
+          } else {
+            const uint32_t vo = vl + c.lr * p.Lmax * 2 + kg * 2 + half * 8 * vstep;
+#pragma unroll
+            for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = ldb64<kCpPlain>(c.vc, vo + d8 * vstep);
+          }
+        }
+        if (npre[h2] < 4) {  // this step's elements from the fragment-ordered copy
+          const uint32_t vo = kg < kend
+                                  ? OFF_VFR + ((((c.g * NSB + st) * 16 + half * 8) * 2 + h2) * 64 + c.lane) * 8
+                                  : OOB;
+          if (npre[h2] == 0) {
+#pragma unroll
+            for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = ldb64<kCpSc1>(c.ws, vo + d8 * 1024);
+          } else {  // the group straddles Lp: merge element-wise
+            const unsigned pm0 = npre[h2] >= 2 ? 0xffffffffu : 0xffffu;
+            const unsigned pm1 = npre[h2] == 3 ? 0xffffu : 0u;
+#pragma unroll
+            for (int d8 = 0; d8 < 8; d8++) {
+              const u32x2 b = ldb64<kCpSc1>(c.ws, vo + d8 * 1024);
+              vf[d8][h2][0] = (vf[d8][h2][0] & pm0) | (b[0] & ~pm0);
+              vf[d8][h2][1] = (vf[d8][h2][1] & pm1) | (b[1] & ~pm1);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int d8 = 0; d8 < 8; d8++) {
+        const int dt = half * 8 + d8;
+        const u32x4 va = {vf[d8][0][0] & vm[0][0], vf[d8][0][1] & vm[0][1], vf[d8][1][0] & vm[1][0],
+                          vf[d8][1][1] & vm[1][1]};
+        o[dt] = mfma16(va, pb, o[dt] * alpha);
+      }
     }
   }
   stamp(c, 24);
@@ -734,13 +804,16 @@ __device__ __forceinline__ void stage_gu(const Params& p, const Ctx& c, int pg0)
   gemm_tok<2, 32>(acc, c, pg0, tv ? OFF_XN + (c.g * TP + t) * D * 2 + c.lq * 16 : OOB, 19);
   page_release(c, pg0 + 4);
   if (!tv) return;
-#pragma unroll
-  for (int rt = 0; rt < 2; rt++) {
-    const f32x4 v = acc[rt];
-    const int f0 = 16 * c.r + 8 * rt + 2 * c.lq;  // local MLP column of the (gate, up) row pairs
-    *reinterpret_cast<unsigned*>(p.ws + OFF_H + ((c.g * TP + t) * 512 + f0) * 2) =
-        pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]);
-  }
+  // h(f) = gelu(gate f) * up f for this CU's 16 columns f = 8rt + 2lq + (0, 1). One exchange with
+  // lane ^ 16 gives every lane 4 consecutive columns, so each token's 32-byte block of the
+  // CU-blocked layout [g][r][t][16] is written whole by 4 lanes (8 bytes each).
+  const unsigned p0 = pack_bf16x2(gelu_tanh(acc[0][0]) * acc[0][1], gelu_tanh(acc[0][2]) * acc[0][3]);
+  const unsigned p1 = pack_bf16x2(gelu_tanh(acc[1][0]) * acc[1][1], gelu_tanh(acc[1][2]) * acc[1][3]);
+  const bool odd = c.lq & 1;
+  const unsigned recv = (unsigned)__shfl_xor((int)(odd ? p0 : p1), 16, 64);
+  const u32x2 out = odd ? u32x2{recv, p1} : u32x2{p0, recv};
+  const int f0 = odd ? 8 + 2 * (c.lq - 1) : 2 * c.lq;
+  *reinterpret_cast<u32x2*>(p.ws + OFF_H + ((c.g * NR + c.r) * TP + t) * 32 + f0 * 2) = out;
 }
 
 // ---------------------------------------------------------------- down (K-window g)
@@ -748,7 +821,10 @@ __device__ __forceinline__ void stage_dn(const Params& p, const Ctx& c, int pg0,
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  if (16 * c.wave < p.Tv) gemm_tok<2, 16>(acc, c, pg0, tv ? OFF_H + (c.g * TP + t) * 512 * 2 + c.lq * 16 : OOB, 21);
+  // X = h in the CU-blocked layout: k = 32ks + 8lq lives in rank 2ks + lq/2, columns 8(lq%2)..
+  if (16 * c.wave < p.Tv)
+    gemm_tok<2, 16, 2 * TP * 32>(
+        acc, c, pg0, tv ? OFF_H + ((c.g * NR + (c.lq >> 1)) * TP + t) * 32 + (c.lq & 1) * 16 : OOB, 21);
   page_release(c, pg0 + 2);
 #pragma unroll
   for (int rt = 0; rt < 2; rt++)
@@ -767,7 +843,6 @@ __device__ __forceinline__ void mark(const Params& p, const Ctx& c, int idx, uin
 
 // ---------------------------------------------------------------- kernel
 __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   Ctx c;
   const int tid = threadIdx.x;
   c.lane = tid & 63;
@@ -776,19 +851,15 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
   c.lq = c.lane >> 4;
   c.g = blockIdx.x & 7;
   c.r = blockIdx.x >> 3;
-  {
-    const int Ltot = p.Lp + p.Tv;
-    c.kb0 = c.r * 32 * ((Ltot + 32 * NCH - 1) / (32 * NCH));
-  }
+  c.kb0 = c.r * 32 * ((p.Lp + p.Tv + 32 * NCH - 1) / (32 * NCH));
   c.ws = make_rsrc(p.ws, WS_BYTES);
   c.kc = make_rsrc(p.kcache, (uint32_t)((size_t)p.NL * p.Lmax * HD * 2));
   c.vc = make_rsrc(p.vtcache, (uint32_t)((size_t)p.NL * p.Lmax * HD * 2));
   c.rc = make_rsrc(p.rope_cos, (uint32_t)(p.Tv * 128 * 4));
   c.rs = make_rsrc(p.rope_sin, (uint32_t)(p.Tv * 128 * 4));
-  c.lds = lds_raw;
-  c.lds_addr = (uint32_t)(uintptr_t)lds_raw;
+  c.lds_addr = (uint32_t)(uintptr_t)fa_lds;
   c.err = reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 8);
-  if (tid < 16) reinterpret_cast<volatile unsigned*>(lds_raw + L_CTL)[tid] = 0u;
+  if (tid < 16) ctl_st(tid, 0u);
   if (tid == 0 && xcc_id() != (unsigned)c.g) atomicOr(c.err, kErrXcd);
   const uint64_t seq = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
   const unsigned xbase =
@@ -804,7 +875,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
   const int NL = p.NL;
   const bool nw = c.wave < 2 && c.r + 32 * c.wave < p.Tv;  // this wave owns a token in norm stages
   if (nw && c.lane < AD)
-    reinterpret_cast<float*>(c.lds + L_XT)[c.wave * AD + c.lane] = p.x_t[(c.r + 32 * c.wave) * AD + c.lane];
+    reinterpret_cast<float*>(fa_lds + L_XT)[c.wave * AD + c.lane] = p.x_t[(c.r + 32 * c.wave) * AD + c.lane];
 
   const float dt = -1.0f / (float)p.S;
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -833,7 +904,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       xcd_sync(p, c);
       mark(p, c, 9, t0);
       stamp(c, 2);
-      stage_qkv(p, c, l, pb + PG_QKV);
+      stage_qkv(p, c, l, pb + PG_QKV, step == p.S - 1);
       stamp(c, 3);
       mark(p, c, 1, t0);
       xcd_sync(p, c);
@@ -880,7 +951,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
     mark(p, c, 8, t0);
   }
   if (c.g == 0 && nw && c.lane < AD)
-    p.x_t[(c.r + 32 * c.wave) * AD + c.lane] = reinterpret_cast<float*>(c.lds + L_XT)[c.wave * AD + c.lane];
+    p.x_t[(c.r + 32 * c.wave) * AD + c.lane] = reinterpret_cast<float*>(fa_lds + L_XT)[c.wave * AD + c.lane];
   if (blockIdx.x == 0 && c.wave == 0 && c.lane == 0) {
     __hip_atomic_store(reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 12), (xbase + (unsigned)(p.S * NL)) & 1u,
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

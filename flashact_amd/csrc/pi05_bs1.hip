@@ -46,18 +46,21 @@ constexpr int NCW = 4, NLW = 2, NTH = 64 * (NCW + NLW);  // compute waves, loade
 constexpr int NCH = 32;                                 // attention key chunks per head
 constexpr int RING = 9, PAGE = 16384, PPL = 13;         // ring pages, page bytes, pages per layer
 constexpr int PG_QKV = 0, PG_K = 4, PG_V = 5, PG_O = 6, PG_GU = 7, PG_DN = 11;
-constexpr int MAXF = 7;                                 // pages in flight per loader wave
+constexpr int MAXF = 1;                                 // pages in flight per loader wave
 constexpr uint32_t OOB = 0x80000000u;                   // buffer offset past every resource
 
 // workspace layout (bytes)
 constexpr uint32_t OFF_CTRL = 0;     // u64 launch sequence, u32 error bits, u32 exchange parity base
 constexpr uint32_t OFF_XFLAG = 1024; // [8 XCD][32 rank][4 wave] u64 epochs
-constexpr uint32_t OFF_XN = 16384;                                  // [8][64][1024] bf16
-constexpr uint32_t OFF_Q = OFF_XN + NX * TP * D * 2;                // [8][64][256] bf16
+// GEMM operands (xn, q, attention output, MLP activation h) are stored in MFMA fragment order:
+// [XCD][token tile of 16][k-step of 32][token % 16][k % 32 / 8][8 bf16], so each 1 KB fragment a
+// wave loads as the B operand is contiguous (see frag_off).
+constexpr uint32_t OFF_XN = 16384;                                  // [8][4][32][16][4][8] bf16
+constexpr uint32_t OFF_Q = OFF_XN + NX * TP * D * 2;                // [8][4][8][16][4][8] bf16
 constexpr uint32_t OFF_ATTP = OFF_Q + NX * TP * HD * 2;             // [8][32][64][256] bf16
 constexpr uint32_t OFF_ATTML = OFF_ATTP + NX * NCH * TP * HD * 2;   // [8][32][64][2] f32
-constexpr uint32_t OFF_ATTN = OFF_ATTML + NX * NCH * TP * 2 * 4;    // [8][64][256] bf16
-constexpr uint32_t OFF_H = OFF_ATTN + NX * TP * HD * 2;             // [8][32 rank][64][16] bf16
+constexpr uint32_t OFF_ATTN = OFF_ATTML + NX * NCH * TP * 2 * 4;    // [8][4][8][16][4][8] bf16
+constexpr uint32_t OFF_H = OFF_ATTN + NX * TP * HD * 2;             // [8][4][16][16][4][8] bf16
 constexpr uint32_t OFF_XP = OFF_H + NX * TP * 512 * 2;              // [2][8][64][1024] f32
 // This step's own keys/values (the suffix) in MFMA fragment order, per 32-key block of the key
 // range: [8 XCD][3 blocks][2 key tiles][8 k-steps][64 lanes][8 bf16] and
@@ -73,6 +76,12 @@ constexpr uint32_t L_CTL = RING * PAGE;        // u32 ready[2], consumed[4], abo
 constexpr uint32_t L_XRES = L_CTL + 64;        // f32 [2][1024] residual stream of tokens r, r+32
 constexpr uint32_t L_XT = L_XRES + 2 * D * 4;  // f32 [2][32] x_t of tokens r, r+32
 constexpr uint32_t LDS_BYTES = L_XT + 2 * AD * 4;
+
+// Byte offset of element (token t, k) of a fragment-ordered operand with KS k-steps of 32,
+// relative to the XCD's block (XCD block size = 64 * 32 * KS * 2 bytes).
+__host__ __device__ constexpr uint32_t frag_off(int KS, int t, int k) {
+  return (uint32_t)(((((t >> 4) * KS + (k >> 5)) * 16 + (t & 15)) * 4 + ((k >> 3) & 3)) * 16 + (k & 7) * 2);
+}
 
 struct Params {
   const bf16* w1;
@@ -326,25 +335,42 @@ __device__ void loader_main(const Params& p, const Ctx& c, int lw) {
 // X[token][k = 8 lq] (OOB for tokens >= Tv: the loads return zeros); k-step ks adds XSTRIDE bytes.
 template <int RT, int KS, int XSTRIDE = 64>
 __device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0, uint32_t xoff, int ts) {
+  // Software-pipelined in chunks of 8 k-steps: the loads of chunk i+1 are in flight while the
+  // MFMAs of chunk i run, so compute starts as soon as the first operands arrive.
   constexpr int NPG = (RT * KS + 15) / 16;
-  u32x4 xf[KS];
+  constexpr int KC = KS < 8 ? KS : 8;
+  constexpr int NCK = KS / KC;
+  u32x4 xf[2][KC];
 #pragma unroll
-  for (int ks = 0; ks < KS; ks++) xf[ks] = ldb128<kCpSc1>(c.ws, xoff + ks * XSTRIDE);
+  for (int k = 0; k < KC; k++) xf[0][k] = ldb128<kCpSc1>(c.ws, xoff + k * XSTRIDE);
+  // two accumulators per row tile (even / odd k-steps) keep four independent MFMA chains in flight
+  f32x4 ac2[RT][2];
 #pragma unroll
-  for (int rt = 0; rt < RT; rt++) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int rt = 0; rt < RT; rt++) ac2[rt][0] = ac2[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   page_wait(c, pg0 + NPG - 1);
   stamp(c, ts);
   uint32_t slot[NPG];
 #pragma unroll
   for (int k = 0; k < NPG; k++) slot[k] = ((pg0 + k) % RING) * PAGE + c.lane * 16;
 #pragma unroll
-  for (int ks = 0; ks < KS; ks++)
+  for (int ck = 0; ck < NCK; ck++) {
+    if (ck + 1 < NCK) {
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-      const int F = rt * KS + ks;
-      const u32x4 a = *reinterpret_cast<const u32x4*>(fa_lds + slot[F >> 4] + (F & 15) * 1024);
-      acc[rt] = mfma16(a, xf[ks], acc[rt]);
+      for (int k = 0; k < KC; k++) xf[(ck + 1) & 1][k] = ldb128<kCpSc1>(c.ws, xoff + ((ck + 1) * KC + k) * XSTRIDE);
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < KC; k++)
+#pragma unroll
+      for (int rt = 0; rt < RT; rt++) {
+        const int F = rt * KS + ck * KC + k;
+        const u32x4 a = *reinterpret_cast<const u32x4*>(fa_lds + slot[F >> 4] + (F & 15) * 1024);
+        ac2[rt][k & 1] = mfma16(a, xf[ck & 1][k], ac2[rt][k & 1]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; rt++) acc[rt] = ac2[rt][0] + ac2[rt][1];
   stamp(c, ts + 1);
 }
 
@@ -475,7 +501,7 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int bu
       const int d = 4 * c.lane + 256 * k;
       *reinterpret_cast<f32x4*>(xres + d) = x[k];
       const u32x2 pk = {pack_bf16x2(h[k][0], h[k][1]), pack_bf16x2(h[k][2], h[k][3])};
-      *reinterpret_cast<u32x2*>(p.ws + OFF_XN + ((c.g * TP + t) * D + d) * 2) = pk;
+      *reinterpret_cast<u32x2*>(p.ws + OFF_XN + c.g * (TP * D * 2) + frag_off(32, t, d)) = pk;
     }
   } else {
     // v[a] = h . W_aout[a] + b_aout[a]; x_t += dt * v   (8 outputs per batch of loads)
@@ -515,7 +541,7 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
     sn[rt] = ldb64<kCpPlain>(c.rs, o);
   }
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  if (any) gemm_tok<2, 32>(acc, c, pg0, tv ? OFF_XN + (c.g * TP + t) * D * 2 + c.lq * 16 : OOB, 15);
+  if (any) gemm_tok<2, 32, 1024>(acc, c, pg0, tv ? OFF_XN + c.g * (TP * D * 2) + frag_off(32, t, 8 * c.lq) : OOB, 15);
   page_release(c, pg0 + 4);
 #pragma unroll
   for (int rt = 0; rt < 2; rt++) {
@@ -546,9 +572,9 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
     const float lo1 = v[2] * c1 - v[3] * s1, hi1 = v[3] * c1 + v[2] * s1;
     const unsigned plo = pack_bf16x2(lo0, lo1), phi = pack_bf16x2(hi0, hi1);
     if (vr0 < 256) {
-      const uint32_t off = OFF_Q + ((c.g * TP + t) * HD + j) * 2;
-      *reinterpret_cast<unsigned*>(p.ws + off) = plo;
-      *reinterpret_cast<unsigned*>(p.ws + off + 256) = phi;
+      const uint32_t qb = OFF_Q + c.g * (TP * HD * 2);
+      *reinterpret_cast<unsigned*>(p.ws + qb + frag_off(8, t, j)) = plo;
+      *reinterpret_cast<unsigned*>(p.ws + qb + frag_off(8, t, j + 128)) = phi;
     } else {
       // Every XCD keeps its own fragment-ordered copy of this step's keys for attention. The
       // caller's cache rows (the reference leaves the last step's suffix K/V there) are written
@@ -595,9 +621,9 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
   const float qscale = 1.4426950408889634f / 16.0f;  // log2(e) / sqrt(256)
   u32x4 qf[8];
   {
-    const uint32_t qb = tv ? OFF_Q + (c.g * TP + t) * HD * 2 + c.lq * 16 : OOB;
+    const uint32_t qb = tv ? OFF_Q + c.g * (TP * HD * 2) + frag_off(8, t, 8 * c.lq) : OOB;
 #pragma unroll
-    for (int ks = 0; ks < 8; ks++) qf[ks] = ldb128<kCpSc1>(c.ws, qb + ks * 64);
+    for (int ks = 0; ks < 8; ks++) qf[ks] = ldb128<kCpSc1>(c.ws, qb + ks * 1024);
   }
   if (kbeg < p.Lp) page_wait(c, pgk + 1);
   stamp(c, 23);
@@ -774,7 +800,7 @@ __device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c) {
       a1 = fmaf(wc, bf_hi(v[ch]), a1);
     }
   }
-  *reinterpret_cast<unsigned*>(p.ws + OFF_ATTN + ((c.g * TP + t) * HD + d0) * 2) = pack_bf16x2(a0, a1);
+  *reinterpret_cast<unsigned*>(p.ws + OFF_ATTN + c.g * (TP * HD * 2) + frag_off(8, t, d0)) = pack_bf16x2(a0, a1);
 }
 
 // ---------------------------------------------------------------- O projection (K-window g)
@@ -784,7 +810,8 @@ __device__ __forceinline__ void stage_oproj(const Params& p, const Ctx& c, int p
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  if (16 * c.wave < p.Tv) gemm_tok<2, 8>(acc, c, pg, tv ? OFF_ATTN + (c.g * TP + t) * HD * 2 + c.lq * 16 : OOB, 17);
+  if (16 * c.wave < p.Tv)
+    gemm_tok<2, 8, 1024>(acc, c, pg, tv ? OFF_ATTN + c.g * (TP * HD * 2) + frag_off(8, t, 8 * c.lq) : OOB, 17);
   page_release(c, pg + 1);
 #pragma unroll
   for (int rt = 0; rt < 2; rt++)
@@ -801,19 +828,18 @@ __device__ __forceinline__ void stage_gu(const Params& p, const Ctx& c, int pg0)
     return;
   }
   f32x4 acc[2];
-  gemm_tok<2, 32>(acc, c, pg0, tv ? OFF_XN + (c.g * TP + t) * D * 2 + c.lq * 16 : OOB, 19);
+  gemm_tok<2, 32, 1024>(acc, c, pg0, tv ? OFF_XN + c.g * (TP * D * 2) + frag_off(32, t, 8 * c.lq) : OOB, 19);
   page_release(c, pg0 + 4);
   if (!tv) return;
   // h(f) = gelu(gate f) * up f for this CU's 16 columns f = 8rt + 2lq + (0, 1). One exchange with
-  // lane ^ 16 gives every lane 4 consecutive columns, so each token's 32-byte block of the
-  // CU-blocked layout [g][r][t][16] is written whole by 4 lanes (8 bytes each).
+  // lane ^ 16 gives every lane 4 consecutive columns, written as 8 bytes of the fragment-ordered h.
   const unsigned p0 = pack_bf16x2(gelu_tanh(acc[0][0]) * acc[0][1], gelu_tanh(acc[0][2]) * acc[0][3]);
   const unsigned p1 = pack_bf16x2(gelu_tanh(acc[1][0]) * acc[1][1], gelu_tanh(acc[1][2]) * acc[1][3]);
   const bool odd = c.lq & 1;
   const unsigned recv = (unsigned)__shfl_xor((int)(odd ? p0 : p1), 16, 64);
   const u32x2 out = odd ? u32x2{recv, p1} : u32x2{p0, recv};
   const int f0 = odd ? 8 + 2 * (c.lq - 1) : 2 * c.lq;
-  *reinterpret_cast<u32x2*>(p.ws + OFF_H + ((c.g * NR + c.r) * TP + t) * 32 + f0 * 2) = out;
+  *reinterpret_cast<u32x2*>(p.ws + OFF_H + c.g * (TP * 512 * 2) + frag_off(16, t, 16 * c.r + f0)) = out;
 }
 
 // ---------------------------------------------------------------- down (K-window g)
@@ -821,10 +847,8 @@ __device__ __forceinline__ void stage_dn(const Params& p, const Ctx& c, int pg0,
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  // X = h in the CU-blocked layout: k = 32ks + 8lq lives in rank 2ks + lq/2, columns 8(lq%2)..
   if (16 * c.wave < p.Tv)
-    gemm_tok<2, 16, 2 * TP * 32>(
-        acc, c, pg0, tv ? OFF_H + ((c.g * NR + (c.lq >> 1)) * TP + t) * 32 + (c.lq & 1) * 16 : OOB, 21);
+    gemm_tok<2, 16, 1024>(acc, c, pg0, tv ? OFF_H + c.g * (TP * 512 * 2) + frag_off(16, t, 8 * c.lq) : OOB, 21);
   page_release(c, pg0 + 2);
 #pragma unroll
   for (int rt = 0; rt < 2; rt++)

@@ -27,6 +27,10 @@ from flashact_amd import pi05, synthetic  # noqa: E402
 NL, D, HD, F, AD = 18, 1024, 256, 4096, 32
 LP, TV, S = 968, 50, 10
 HBM_PEAK_GBS = 8000.0
+# L2 <-> memory bytes of one pi05_denoise_bs1 launch at this workload, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes scaled by a 1 GiB device copy (profiles/pi05_denoise_bs1_traffic.md). Counters
+# cannot be read inside a timed run, so the figure is the last measured one for this kernel.
+TRAFFIC_BYTES = {"fetch": 15_709_937_267, "write": 2_475_342_645}
 
 
 def algorithmic_bytes_per_chunk(nl=NL, lp=LP, tv=TV, s=S) -> int:
@@ -81,12 +85,22 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline and parity check")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="first run a plain device copy of this many bytes (twice), the calibration dispatch for "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the pi0.5/MolmoAct2 denoise loop is a single-GPU "
                                    "kernel (batch-DP sharding needs no exchange; see DESIGN.md)", "n_gpus": args.gpus}))
         sys.exit(2)
     dev = torch.device("cuda:0")
+    if args.copy_bytes > 0:
+        src = torch.ones(args.copy_bytes // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     w, inp, mods, modf, packed, cos, sin, Lmax, kc, vc = build_inputs(dev)
     x_t = inp["noise"][0].clone()
     empty = torch.empty(0, device=dev)
@@ -136,7 +150,8 @@ def main():
         "config": {"workload": "pi05_expert_bs1_T50_Lp968_S10", "layers": NL, "batch": 1, "action_tokens": TV,
                    "prefix_len": LP, "euler_steps": S, "launches_per_chunk": 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": TRAFFIC_BYTES["fetch"] + TRAFFIC_BYTES["write"], "traffic_split": TRAFFIC_BYTES,
                      "algorithmic_bytes": nbytes, "kernel_ms_mean": round(kern_ms, 4),
                      "kernel_ms_p50": round(float(np.median(per)), 4), "kernel_ms_min": round(float(per.min()), 4)},
         "wall_ms_per_step": round(t_wall * 1000.0 / args.steps, 4),

@@ -1,0 +1,219 @@
+// Stage engine of the batched denoise kernels (MFMA-bound regime: M = batch x Tv tokens).
+//
+// One cooperative launch of 256 workgroups (one per CU) x 256 threads (4 waves). The loop is a
+// fixed sequence of stages separated by grid barriers; inside a stage the workgroups take work
+// items (GEMM tiles, attention blocks, rows) round robin in an XCD-major order, so consecutive
+// items (which share a weight tile) run on the CUs of one XCD and hit that XCD's L2.
+//
+// Every intermediate crosses XCDs, so intermediates are stored with sc1 (write-through) and read
+// with sc1 (buffer loads, or global_load_lds ... sc1 for GEMM operands); weights and the prefix
+// K/V are read-only inputs.
+#pragma once
+#include "fa_device.h"
+
+namespace fa {
+namespace eng {
+
+constexpr int NWG = 256;   // workgroups (one per CU)
+constexpr int NTHR = 256;  // threads per workgroup (4 waves)
+
+extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// XCD-major virtual workgroup index: workgroup b runs on XCD b % 8; v = xcd * 32 + rank.
+__device__ __forceinline__ int vwg() { return (blockIdx.x & 7) * 32 + (blockIdx.x >> 3); }
+
+// ---------------------------------------------------------------- global <-> LDS copies
+// global_load_lds_dwordx4: lane i copies 16 bytes from its address to LDS m0 + 16 i, so one
+// instruction lands one 1 KB MFMA fragment in lane order. m0 is saved and restored.
+template <bool SC1>
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
+  unsigned saved;
+  if (SC1)
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off sc1\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+                 : "memory");
+  else
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+                 : "memory");
+}
+
+#define FA_ENG_VMCNT(n) (((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  __builtin_amdgcn_s_waitcnt(FA_ENG_VMCNT(N));
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(uint32_t off) { return (uint32_t)(uintptr_t)lds + off; }
+__device__ __forceinline__ u32x4 lds128(uint32_t off) { return *reinterpret_cast<const u32x4*>(lds + off); }
+
+// sc1 stores through a buffer resource (base must be wave-uniform; offsets in bytes).
+__device__ __forceinline__ void st_b128(rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCpSc1);
+}
+__device__ __forceinline__ void st_b64(rsrc_t r, uint32_t off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, kCpSc1);
+}
+__device__ __forceinline__ void st_b32(rsrc_t r, uint32_t off, unsigned v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kCpSc1);
+}
+__device__ __forceinline__ void st_b16(rsrc_t r, uint32_t off, unsigned short v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kCpSc1);
+}
+__device__ __forceinline__ rsrc_t rsrc_all(const void* base) { return make_rsrc(base, 0xffffffffu); }
+
+// ---------------------------------------------------------------- grid barrier
+// Flat epoch barrier: every workgroup stores its epoch (sc1) to its own slot of a 256-entry line;
+// wave 0 polls the whole line (4 slots per lane, sc1) until every slot holds >= the epoch. One
+// cross-XCD round trip per barrier. The wait is capped; a cap hit sets a sticky error bit that
+// makes every later wait return at once.
+struct Grid {
+  uint64_t* flags;  // [256] u64
+  unsigned* err;
+  uint64_t e;
+};
+
+__device__ __forceinline__ void grid_sync(Grid& g) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
+  __syncthreads();
+  g.e += 1;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(g.flags + blockIdx.x, g.e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x < 64 && !(__hip_atomic_load(g.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin)) {
+    const rsrc_t r = make_rsrc(g.flags, NWG * 8);
+    const uint32_t off = (threadIdx.x & 63) * 32;
+    for (unsigned it = 0;; ++it) {
+      const u32x4 a = ldb128<kCpSc1>(r, off), b = ldb128<kCpSc1>(r, off + 16);
+      const uint64_t f0 = ((uint64_t)a[1] << 32) | a[0], f1 = ((uint64_t)a[3] << 32) | a[2];
+      const uint64_t f2 = ((uint64_t)b[1] << 32) | b[0], f3 = ((uint64_t)b[3] << 32) | b[2];
+      const bool ok = f0 >= g.e && f1 >= g.e && f2 >= g.e && f3 >= g.e;
+      if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+      if (it > kSpinCap) {
+        if ((threadIdx.x & 63) == 0) atomicOr(g.err, kErrSpin);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+  asm volatile("" ::: "memory");
+}
+
+// ---------------------------------------------------------------- tiled GEMM
+// C^T[n][m] = sum_k W[n][k] A[m][k] over k in [k0, k1) for a BM x BN tile (BM = 32 WM, BN = 32 WN).
+// Waves form a 2 x 2 grid; wave (wm, wn) computes WM x WN MFMA blocks of 16 x 16 with
+// v_mfma_f32_16x16x32_bf16 (A operand = 16 weight rows, B operand = 16 tokens), so after the loop
+// lane l holds, for block (j, i), rows n = 16 (wn WN + j) + 4 (l / 16) + 0..3 of token
+// m = 16 (wm WM + i) + l % 16 -- four consecutive output features of one token.
+// Operands are staged per 64-k step in MFMA fragment order by global_load_lds (3-buffer ring, one
+// workgroup barrier per step). Rows m >= M copy row 0 (their results are discarded).
+struct GemmArgs {
+  const bf16* A;  // [M][lda] activations (written in this launch: sc1 copies)
+  const bf16* W;  // [N][ldw] weights
+  int lda, ldw, M;
+};
+
+template <int WM, int WN>
+struct GemmShape {
+  static constexpr int BM = 32 * WM, BN = 32 * WN;
+  static constexpr int NA = BM / 8, NW = BN / 8, NF = NA + NW;  // 1 KB fragments per 64-k step
+  static constexpr int FPW = NF / 4;                              // fragments per wave per step
+  static constexpr uint32_t STEP = NF * 1024;
+  static constexpr uint32_t LDS = 3 * STEP;
+};
+
+template <int WM, int WN, class Epi>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int k0, int k1, Epi& epi) {
+  using S = GemmShape<WM, WN>;
+  const int w = wave_id(), lane = lane_id(), lr = lane & 15, lq = lane >> 4;
+  const int wm = w & 1, wn = w >> 1;
+  // this wave's fragments of every step: f = w + 4 j
+  const unsigned char* src[S::FPW];
+#pragma unroll
+  for (int j = 0; j < S::FPW; j++) {
+    const int f = w + 4 * j;
+    if (f < S::NA) {
+      int row = m0 + 16 * (f >> 1) + lr;
+      if (row >= g.M) row = 0;
+      src[j] = reinterpret_cast<const unsigned char*>(g.A + (size_t)row * g.lda + k0 + 32 * (f & 1) + 8 * lq);
+    } else {
+      const int fw = f - S::NA;
+      const int row = n0 + 16 * (fw >> 1) + lr;
+      src[j] = reinterpret_cast<const unsigned char*>(g.W + (size_t)row * g.ldw + k0 + 32 * (fw & 1) + 8 * lq);
+    }
+  }
+  const int ns = (k1 - k0) >> 6;
+  auto issue = [&](int s) {
+    const uint32_t base = (uint32_t)(s % 3) * S::STEP;
+#pragma unroll
+    for (int j = 0; j < S::FPW; j++) {
+      const int f = w + 4 * j;
+      if (f < S::NA)
+        dma16<true>(src[j] + 128 * s, lds_addr(base + f * 1024));
+      else
+        dma16<false>(src[j] + 128 * s, lds_addr(base + f * 1024));
+    }
+  };
+  f32x4 acc[WN][WM];
+#pragma unroll
+  for (int j = 0; j < WN; j++)
+#pragma unroll
+    for (int i = 0; i < WM; i++) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  __builtin_amdgcn_s_waitcnt(0);  // earlier stores / loads of this wave are complete
+  issue(0);
+  if (ns > 1) issue(1);
+#pragma unroll 1
+  for (int s = 0; s < ns; s++) {
+    if (s + 1 < ns)
+      vm_wait<S::FPW>();
+    else
+      vm_wait<0>();
+    __syncthreads();  // step s landed for every wave; every wave is done with step s - 1
+    if (s + 2 < ns) issue(s + 2);
+    const uint32_t base = (uint32_t)(s % 3) * S::STEP;
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      u32x4 a[WM], b[WN];
+#pragma unroll
+      for (int i = 0; i < WM; i++) a[i] = lds128(base + ((wm * WM + i) * 2 + ks) * 1024 + lane * 16);
+#pragma unroll
+      for (int j = 0; j < WN; j++) b[j] = lds128(base + (S::NA + (wn * WN + j) * 2 + ks) * 1024 + lane * 16);
+#pragma unroll
+      for (int j = 0; j < WN; j++)
+#pragma unroll
+        for (int i = 0; i < WM; i++) acc[j][i] = mfma16(b[j], a[i], acc[j][i]);
+    }
+  }
+  __syncthreads();  // the ring is free for the next tile
+#pragma unroll
+  for (int j = 0; j < WN; j++)
+#pragma unroll
+    for (int i = 0; i < WM; i++) {
+      const int m = m0 + 16 * (wm * WM + i) + lr;
+      if (m < g.M) epi(n0 + 16 * (wn * WN + j) + 4 * lq, m, acc[j][i]);
+    }
+}
+
+// Runs every tile of an [M x N] GEMM, K split into `ksplit` equal ranges (multiples of 64). Items
+// are ordered m-tile fastest so the items of one weight tile run on neighbouring CUs of one XCD.
+// The epilogue receives the split index through epi.split.
+template <int WM, int WN, class Epi>
+__device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int ksplit, Epi& epi) {
+  using S = GemmShape<WM, WN>;
+  const int nm = (g.M + S::BM - 1) / S::BM, nn = N / S::BN;
+  const int items = nm * nn * ksplit, kc = K / ksplit;
+#pragma unroll 1
+  for (int it = vwg(); it < items; it += NWG) {
+    const int mt = it % nm, rest = it / nm, nt = rest % nn, sp = rest / nn;
+    epi.split = sp;
+    gemm_tile<WM, WN>(g, mt * S::BM, nt * S::BN, sp * kc, sp * kc + kc, epi);
+  }
+}
+
+}  // namespace eng
+}  // namespace fa

@@ -87,6 +87,7 @@ __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
   bf16x2 v = {(bf16)a, (bf16)b};
   return __builtin_bit_cast(unsigned, v);
 }
+__device__ __forceinline__ unsigned short bf16_bits(float a) { return __builtin_bit_cast(unsigned short, (bf16)a); }
 __device__ __forceinline__ float bf_lo(unsigned u) { return __builtin_bit_cast(float, u << 16); }
 __device__ __forceinline__ float bf_hi(unsigned u) { return __builtin_bit_cast(float, u & 0xffff0000u); }
 

@@ -5,6 +5,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include "../../include/flashact_mi355x.h"
+
 namespace fa {
 namespace host {
 
@@ -24,4 +26,9 @@ inline int fail(int code, const char* fmt, ...) {
 int check_device(const void* kernel, int threads, unsigned lds_bytes, int nwg, const char* who);
 
 }  // namespace host
+
+// Batched pi0.5 launch (batch >= 2), dispatched from fa_pi05_denoise after the shared checks.
+size_t pi05_batched_workspace_bytes(int batch, int Tv, int Lmax);
+int pi05_denoise_batched(const fa_pi05_args* a, fa_stream_t stream);
+
 }  // namespace fa

@@ -1,0 +1,574 @@
+// pi0.5 action-expert denoise loop for a batch of samples (batch 16, M = 800
+// action tokens per GEMM): the whole S-step Euler loop in ONE cooperative launch of 256
+// workgroups x 4 waves, built on the stage engine (engine.h). This is the MFMA-bound regime, so
+// the GEMMs are 128-token tiles over all samples at once.
+//
+// Per layer (grid barrier after each stage), token m = b * Tv + t of sample b:
+//   N1   x = embed(x_t) (layer 0) or x += gate_post * sum(down partials); xn = adaRMS(x)
+//   QKV  [M x 2560] = xn W1^T; RoPE; q -> per-sample fragment-ordered Q; k, v -> the caller's
+//        caches (row / column Lp + t of layer l), as the reference does (src/pi05/mk6.cu:307-310)
+//   ATT  per (sample, 128-key chunk, group of 16 query tiles): MQA over the chunk (8 heads x Tv
+//        query rows share the one K/V head), online softmax, normalised partial O + (m, l)
+//   COMB flash-decoding combine of the key chunks -> attn [M x 2048]
+//   O    [M x 1024] = attn Wo^T, K split 4 ways -> fp32 partials
+//   N2   x += gate_in * sum(partials); xn = adaRMS(x)
+//   GU   [M x 8192] = xn W2^T (gate/up rows interleaved) -> h = gelu_tanh(g) u [M x 4096]
+//   DN   [M x 1024] = h W3^T, K split 4 ways -> fp32 partials
+// then the final norm, action projection and Euler update (src/pi05/mk6.cu:502-517).
+#include "engine.h"
+#include "../../include/flashact_mi355x.h"
+#include "fa_host.h"
+
+namespace fa {
+namespace pb {
+using namespace fa::eng;
+
+constexpr int D = 1024, HD = 256, AD = 32, NH = 8, QD = 2048, FF = 4096;
+constexpr int KSPLIT = 4;    // K split of the O and down projections
+constexpr int KCH = 128;     // keys per attention chunk
+constexpr int QTG = 16;      // query tiles (16 rows) per attention item
+constexpr int MAX_TOKENS = 4096;
+
+// Workspace layout (bytes), a function of (B, Tv, Lmax).
+struct Layout {
+  int B, Tv, M, MP, NQT, NKC;
+  size_t x, xn, qf, attp, ml, attn, h, part, total;
+};
+__host__ __device__ inline Layout layout(int B, int Tv, int Lmax) {
+  Layout L;
+  L.B = B;
+  L.Tv = Tv;
+  L.M = B * Tv;
+  L.MP = (L.M + 127) / 128 * 128;
+  L.NQT = (NH * Tv + 15) / 16;
+  L.NKC = (Lmax + KCH - 1) / KCH;
+  size_t o = 4096;  // control block + 256 barrier slots
+  auto take = [&](size_t n) {
+    const size_t r = o;
+    o += (n + 255) / 256 * 256;
+    return r;
+  };
+  L.x = take((size_t)L.MP * D * 4);
+  L.xn = take((size_t)L.MP * D * 2);
+  L.qf = take((size_t)B * L.NQT * 16 * HD * 2);
+  L.attp = take((size_t)B * L.NKC * L.NQT * 16 * HD * 2);
+  L.ml = take((size_t)B * L.NKC * L.NQT * 16 * 8);
+  L.attn = take((size_t)L.MP * QD * 2);
+  L.h = take((size_t)L.MP * FF * 2);
+  L.part = take((size_t)KSPLIT * L.MP * D * 4);
+  L.total = o;
+  return L;
+}
+constexpr uint32_t OFF_CTRL = 0, OFF_FLAGS = 1024;
+
+struct Params {
+  const bf16* w1;
+  const bf16* wo;
+  const bf16* w2;
+  const bf16* w3;
+  const float* mods;
+  const float* mod_final;
+  const float* rope_cos;
+  const float* rope_sin;
+  const float* w_ain;
+  const float* b_ain;
+  const float* w_aout;
+  const float* b_aout;
+  bf16* kcache;  // [B][NL][Lmax][256]
+  bf16* vtcache; // [B][NL][256][Lmax]
+  float* x_t;    // [B][xt_rows][32]
+  unsigned long long* stage_cycles;
+  unsigned char* ws;
+  Layout L;
+  int NL, Lp, Lmax, S, Tv, B, xt_rows;
+};
+
+// Fragment-ordered Q of sample b: row r = h * Tv + t, dim d -> tile r/16, k-step d/32, lane
+// (r % 16) + 16 ((d % 32) / 8), element d % 8.
+__host__ __device__ inline uint32_t qf_off(int NQT, int b, int r, int d) {
+  return (uint32_t)(((((size_t)b * NQT + (r >> 4)) * 8 + (d >> 5)) * 64 + (r & 15) + 16 * ((d & 31) >> 3)) * 16 +
+                    (d & 7) * 2);
+}
+
+// ---------------------------------------------------------------- GEMM epilogues
+struct EpiQKV {  // RoPE on q/k pairs (rows 2p, 2p+1 = dims j, j+128), q -> Qf, k/v -> caches
+  rsrc_t ws, kc, vc;
+  const float* rcos;
+  const float* rsin;
+  uint32_t qf;
+  int NQT, Tv, NL, Lmax, Lp, l, split;
+  __device__ void operator()(int n0, int m, f32x4 v) const {
+    const int b = m / Tv, t = m - b * Tv;
+    if (n0 >= 2304) {  // v rows: dims n0-2304 .. +3 of key Lp+t
+      const int d0 = n0 - 2304;
+      const size_t base = (((size_t)b * NL + l) * HD + d0) * Lmax + Lp + t;
+#pragma unroll
+      for (int i = 0; i < 4; i++) st_b16(vc, (uint32_t)((base + (size_t)i * Lmax) * 2), bf16_bits(v[i]));
+      return;
+    }
+    const int p0 = (n0 < 2048 ? n0 : n0 - 2048) >> 1;  // first of two RoPE pairs
+    const int j0 = p0 & 127;
+    const float c0 = rcos[t * 128 + j0], c1 = rcos[t * 128 + j0 + 1];
+    const float s0 = rsin[t * 128 + j0], s1 = rsin[t * 128 + j0 + 1];
+    const float lo0 = v[0] * c0 - v[1] * s0, hi0 = v[1] * c0 + v[0] * s0;
+    const float lo1 = v[2] * c1 - v[3] * s1, hi1 = v[3] * c1 + v[2] * s1;
+    const unsigned plo = pack_bf16x2(lo0, lo1), phi = pack_bf16x2(hi0, hi1);
+    if (n0 < 2048) {
+      const int r = (p0 >> 7) * Tv + t;
+      st_b32(ws, qf + qf_off(NQT, b, r, j0), plo);
+      st_b32(ws, qf + qf_off(NQT, b, r, j0 + 128), phi);
+    } else {
+      const size_t row = (((size_t)b * NL + l) * Lmax + Lp + t) * HD;
+      st_b32(kc, (uint32_t)((row + j0) * 2), plo);
+      st_b32(kc, (uint32_t)((row + j0 + 128) * 2), phi);
+    }
+  }
+};
+
+struct EpiGelu {  // rows 2f, 2f+1 = gate f, up f -> h[m][f] = gelu_tanh(g) u
+  rsrc_t ws;
+  uint32_t off;
+  int split;
+  __device__ void operator()(int n0, int m, f32x4 v) const {
+    const unsigned pk = pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]);
+    st_b32(ws, off + (uint32_t)(((size_t)m * FF + (n0 >> 1)) * 2), pk);
+  }
+};
+
+struct EpiPart {  // fp32 partial sums [split][MP][1024]
+  rsrc_t ws;
+  uint32_t off;
+  int MP, split;
+  __device__ void operator()(int n0, int m, f32x4 v) const {
+    st_b128(ws, off + (uint32_t)((((size_t)split * MP + m) * D + n0) * 4), as_u32x4(v));
+  }
+};
+
+// ---------------------------------------------------------------- norm rows
+// One wave per token row; lane holds columns 4 lane + 256 k + i. MODE 0: x = embed(x_t);
+// MODE 1: x += gate * sum of the K-split partials; MODE 2: as 1, then final norm + action
+// projection + Euler update of x_t.
+template <int MODE>
+__device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xtr, const float* gate, const float* scale, const float* shift,
+                           float dt) {
+  const Layout& L = p.L;
+  const int lane = lane_id();
+  const int nwave = NWG * 4;
+#pragma unroll 1
+  for (int m = vwg() * 4 + wave_id(); m < L.M; m += nwave) {
+    const int b = m / p.Tv, t = m - b * p.Tv;
+    const uint32_t xto = (uint32_t)(((size_t)b * p.xt_rows + t) * AD * 4);
+    f32x4 x[4];
+    if (MODE == 0) {
+      const float xl = lane < AD ? ldbf32<kCpSc1>(xtr, xto + lane * 4) : 0.f;
+      float xa[AD];
+#pragma unroll
+      for (int a = 0; a < AD; a++) xa[a] = __shfl(xl, a, 64);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int d = 4 * lane + 256 * k;
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(p.b_ain + d);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          float s = bb[i];
+#pragma unroll
+          for (int q = 0; q < 8; q++) {
+            const f32x4 wv = *reinterpret_cast<const f32x4*>(p.w_ain + (d + i) * AD + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; e++) s = fmaf(wv[e], xa[4 * q + e], s);
+          }
+          x[k][i] = s;
+        }
+      }
+    } else {
+      u32x4 pr[KSPLIT][4], xo[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int d = 4 * lane + 256 * k;
+        xo[k] = ldb128<kCpSc1>(ws, (uint32_t)(L.x + ((size_t)m * D + d) * 4));
+#pragma unroll
+        for (int s = 0; s < KSPLIT; s++)
+          pr[s][k] = ldb128<kCpSc1>(ws, (uint32_t)(L.part + (((size_t)s * L.MP + m) * D + d) * 4));
+      }
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int d = 4 * lane + 256 * k;
+        f32x4 s = as_f32x4(pr[0][k]);
+#pragma unroll
+        for (int sp = 1; sp < KSPLIT; sp++) s += as_f32x4(pr[sp][k]);
+        const f32x4 gt = *reinterpret_cast<const f32x4*>(gate + d);
+        x[k] = as_f32x4(xo[k]) + gt * s;
+      }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) ss += x[k][0] * x[k][0] + x[k][1] * x[k][1] + x[k][2] * x[k][2] + x[k][3] * x[k][3];
+    const float rr = rsqrtf(wave_sum(ss) / (float)D + 1e-6f);
+    f32x4 h[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int d = 4 * lane + 256 * k;
+      const f32x4 sc = *reinterpret_cast<const f32x4*>(scale + d);
+      const f32x4 sh = *reinterpret_cast<const f32x4*>(shift + d);
+#pragma unroll
+      for (int i = 0; i < 4; i++) h[k][i] = x[k][i] * rr * (1.0f + sc[i]) + sh[i];
+    }
+    if (MODE != 2) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int d = 4 * lane + 256 * k;
+        st_b128(ws, (uint32_t)(L.x + ((size_t)m * D + d) * 4), as_u32x4(x[k]));
+        st_b64(ws, (uint32_t)(L.xn + ((size_t)m * D + d) * 2),
+               u32x2{pack_bf16x2(h[k][0], h[k][1]), pack_bf16x2(h[k][2], h[k][3])});
+      }
+    } else {
+      float acc = 0.f;  // lane a < 32 ends with v[a]
+#pragma unroll 1
+      for (int a0 = 0; a0 < AD; a0 += 8) {
+        f32x4 wv[8][4];
+#pragma unroll
+        for (int a = 0; a < 8; a++)
+#pragma unroll
+          for (int k = 0; k < 4; k++)
+            wv[a][k] = *reinterpret_cast<const f32x4*>(p.w_aout + (a0 + a) * D + 4 * lane + 256 * k);
+#pragma unroll
+        for (int a = 0; a < 8; a++) {
+          float s = 0.f;
+#pragma unroll
+          for (int k = 0; k < 4; k++)
+            s += wv[a][k][0] * h[k][0] + wv[a][k][1] * h[k][1] + wv[a][k][2] * h[k][2] + wv[a][k][3] * h[k][3];
+          s = wave_sum(s);
+          if (lane == a0 + a) acc = s;
+        }
+      }
+      if (lane < AD) {
+        const float xo = ldbf32<kCpSc1>(xtr, xto + lane * 4);
+        __builtin_amdgcn_raw_buffer_store_b32(as_u32(xo + dt * (acc + p.b_aout[lane])), xtr, xto + lane * 4, 0, kCpSc1);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- attention partials
+// Item (b, kc, qg): keys [128 kc, 128 kc + 128) of sample b against query tiles 16 qg + w + 4 j
+// (wave w, j < 4, processed one after the other). The chunk's K rows and V^T columns are copied
+// to LDS once, in MFMA fragment order (64 + 64 fragments). K rows are permuted inside each 32-key
+// span so that the S^T accumulators of key tiles (2 sp, 2 sp + 1) are directly the P^T operand of
+// k-step sp: tile row 4a + i of key tile 2 sp + kt holds key 32 sp + 8 a + 4 kt + i.
+// Keys >= Ltot: S = -inf and their V^T elements are zeroed.
+constexpr uint32_t ATT_LDS = 128 * 1024;
+
+__device__ __forceinline__ void stage_att(const Params& p, rsrc_t ws, int l) {
+  const Layout& L = p.L;
+  const int w = wave_id(), lane = lane_id(), lr = lane & 15, lq = lane >> 4;
+  const int Ltot = p.Lp + p.Tv;
+  const int nkc = (Ltot + KCH - 1) / KCH, nqg = (L.NQT + QTG - 1) / QTG;
+  const int items = p.B * nkc * nqg;
+  const float qscale = 1.4426950408889634f / 16.0f;  // log2(e) / sqrt(256)
+#pragma unroll 1
+  for (int it = vwg(); it < items; it += NWG) {
+    const int qg = it % nqg, rest = it / nqg, kc = rest % nkc, b = rest / nkc;
+    const int key0 = kc * KCH, kend = min(key0 + KCH, Ltot);
+    const bf16* kb_ = p.kcache + ((size_t)b * p.NL + l) * p.Lmax * HD;
+    const bf16* vb_ = p.vtcache + ((size_t)b * p.NL + l) * HD * p.Lmax;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // the previous item's readers are done with LDS
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      const int f = w + 4 * j;
+      if (f < 64) {  // K fragment (key tile kt8 = f / 8, k-step f % 8)
+        const int kt8 = f >> 3, ks = f & 7;
+        int key = key0 + 32 * (kt8 >> 1) + 8 * (lr >> 2) + 4 * (kt8 & 1) + (lr & 3);
+        if (key >= Ltot) key = 0;
+        dma16<true>(kb_ + (size_t)key * HD + ks * 32 + 8 * lq, lds_addr(f * 1024));
+      } else {  // V^T fragment (dim tile dt, 32-key span sp)
+        const int fv = f - 64, dt = fv >> 2, sp = fv & 3;
+        int kg = key0 + 32 * sp + 8 * lq;
+        if (kg >= Ltot) kg = 0;
+        dma16<true>(vb_ + (size_t)(16 * dt + lr) * p.Lmax + kg, lds_addr(f * 1024));
+      }
+    }
+    unsigned vmask[4][4];  // V^T element masks of keys >= kend
+#pragma unroll
+    for (int sp = 0; sp < 4; sp++) {
+      const int nv = min(max(kend - (key0 + 32 * sp + 8 * lq), 0), 8);
+#pragma unroll
+      for (int e = 0; e < 4; e++) vmask[sp][e] = nv >= 2 * e + 2 ? 0xffffffffu : (nv == 2 * e + 1 ? 0xffffu : 0u);
+    }
+    vm_wait<0>();
+    __syncthreads();
+#pragma unroll 1
+    for (int j = 0; j < QTG / 4; j++) {
+      const int qt = QTG * qg + w + 4 * j;
+      if (qt >= L.NQT) break;
+      u32x4 qf[8];
+#pragma unroll
+      for (int ks = 0; ks < 8; ks++)
+        qf[ks] = ldb128<kCpSc1>(ws, (uint32_t)(L.qf + ((((size_t)b * L.NQT + qt) * 8 + ks) * 64 + lane) * 16));
+      f32x4 s[8];
+#pragma unroll
+      for (int kt8 = 0; kt8 < 8; kt8++) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) a = mfma16(lds128((kt8 * 8 + ks) * 1024 + lane * 16), qf[ks], a);
+        s[kt8] = a;
+      }
+      float mx = -1e30f;
+#pragma unroll
+      for (int kt8 = 0; kt8 < 8; kt8++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int key = key0 + 32 * (kt8 >> 1) + 8 * lq + 4 * (kt8 & 1) + i;
+          s[kt8][i] = key < kend ? s[kt8][i] * qscale : -1e30f;
+          mx = fmaxf(mx, s[kt8][i]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      float psum = 0.f;
+      u32x4 pb[4];
+#pragma unroll
+      for (int sp = 0; sp < 4; sp++) {
+        float pv[8];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            pv[4 * kt + i] = exp2f(s[2 * sp + kt][i] - mx);
+            psum += pv[4 * kt + i];
+          }
+        pb[sp] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                       pack_bf16x2(pv[6], pv[7])};
+      }
+      psum += __shfl_xor(psum, 16, 64);
+      psum += __shfl_xor(psum, 32, 64);
+      f32x4 o[16];
+#pragma unroll
+      for (int dt = 0; dt < 16; dt++) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int sp = 0; sp < 4; sp++) {
+          u32x4 va = lds128((64 + dt * 4 + sp) * 1024 + lane * 16);
+#pragma unroll
+          for (int e = 0; e < 4; e++) va[e] &= vmask[sp][e];
+          acc = mfma16(va, pb[sp], acc);
+        }
+        o[dt] = acc;
+      }
+      // lane holds O^T[dim 16 dt + 4 lq + i][query row 16 qt + lr]
+      const int r = 16 * qt + lr;
+      if (r < NH * p.Tv) {
+        const float inv = 1.0f / psum;
+        const size_t prow = ((size_t)b * L.NKC + kc) * L.NQT * 16 + r;
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++)
+          st_b64(ws, (uint32_t)(L.attp + (prow * HD + 16 * dt + 4 * lq) * 2),
+                 u32x2{pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv), pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv)});
+        if (lq == 0) st_b64(ws, (uint32_t)(L.ml + prow * 8), u32x2{as_u32(mx), as_u32(psum)});
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- combine
+// One wave per (sample, query row): attn[b Tv + t][256 h + d] = sum_c w_c O_c, w_c ~ l_c 2^(m_c - M).
+__device__ __forceinline__ void stage_comb(const Params& p, rsrc_t ws) {
+  const Layout& L = p.L;
+  const int lane = lane_id();
+  const int Ltot = p.Lp + p.Tv, nkc = (Ltot + KCH - 1) / KCH;
+  const int rows = p.B * NH * p.Tv;
+#pragma unroll 1
+  for (int R = vwg() * 4 + wave_id(); R < rows; R += NWG * 4) {
+    const int b = R / (NH * p.Tv), r = R - b * NH * p.Tv, h = r / p.Tv, t = r - h * p.Tv;
+    float mc = -1e30f, lc = 0.f;
+    if (lane < nkc) {
+      const u32x2 ml = ldb64<kCpSc1>(ws, (uint32_t)(L.ml + ((((size_t)b * L.NKC + lane) * L.NQT * 16) + r) * 8));
+      mc = as_f32(ml[0]);
+      lc = as_f32(ml[1]);
+    }
+    const float Mx = wave_max(mc);
+    const float wgt = lc * exp2f(mc - Mx);
+    const float wn = wgt / wave_sum(wgt);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int c = 0; c < nkc; c++) {
+      const float wc = __shfl(wn, c, 64);
+      const u32x2 v = ldb64<kCpSc1>(ws, (uint32_t)(L.attp + ((((size_t)b * L.NKC + c) * L.NQT * 16 + r) * HD + 4 * lane) * 2));
+      acc[0] = fmaf(wc, bf_lo(v[0]), acc[0]);
+      acc[1] = fmaf(wc, bf_hi(v[0]), acc[1]);
+      acc[2] = fmaf(wc, bf_lo(v[1]), acc[2]);
+      acc[3] = fmaf(wc, bf_hi(v[1]), acc[3]);
+    }
+    const int m = b * p.Tv + t;
+    st_b64(ws, (uint32_t)(L.attn + ((size_t)m * QD + h * HD + 4 * lane) * 2),
+           u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])});
+  }
+}
+
+// ---------------------------------------------------------------- the kernel
+constexpr uint32_t LDS_BYTES = GemmShape<4, 8>::LDS;  // 144 KB: the largest stage footprint
+static_assert(GemmShape<4, 4>::LDS <= LDS_BYTES && ATT_LDS <= LDS_BYTES, "LDS budget");
+
+__device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {
+  if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x == 0) {
+    const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+    p.stage_cycles[idx] += t1 - t0;
+    t0 = t1;
+  }
+}
+
+__global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
+  const Layout& L = p.L;
+  const rsrc_t ws = rsrc_all(p.ws);
+  const rsrc_t kc = rsrc_all(p.kcache);
+  const rsrc_t vc = rsrc_all(p.vtcache);
+  const rsrc_t xtr = make_rsrc(p.x_t, (uint32_t)((size_t)p.B * p.xt_rows * AD * 4));
+  Grid grid;
+  grid.flags = reinterpret_cast<uint64_t*>(p.ws + OFF_FLAGS);
+  grid.err = reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 8);
+  const uint64_t seq = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
+  grid.e = seq << 32;
+  const int NL = p.NL;
+  const float dt = -1.0f / (float)p.S;
+  uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x < 16) p.stage_cycles[threadIdx.x] = 0;
+  GemmArgs gx{reinterpret_cast<const bf16*>(p.ws + L.xn), nullptr, D, D, L.M};
+  GemmArgs ga{reinterpret_cast<const bf16*>(p.ws + L.attn), nullptr, QD, QD, L.M};
+  GemmArgs gh{reinterpret_cast<const bf16*>(p.ws + L.h), nullptr, FF, FF, L.M};
+#pragma unroll 1
+  for (int step = 0; step < p.S; step++) {
+#pragma unroll 1
+    for (int l = 0; l < NL; l++) {
+      const int li = step * NL + l;
+      const float* mod_in = p.mods + ((size_t)li * 2 + 0) * 3 * D;
+      const float* mod_post = p.mods + ((size_t)li * 2 + 1) * 3 * D;
+      if (l == 0)
+        stage_norm<0>(p, ws, xtr, nullptr, mod_in, mod_in + D, 0.f);
+      else
+        stage_norm<1>(p, ws, xtr, mod_post - 6 * D + 2 * D, mod_in, mod_in + D, 0.f);
+      mark(p, 0, t0);
+      grid_sync(grid);
+      mark(p, 9, t0);
+      {
+        EpiQKV e{ws, kc, vc, p.rope_cos, p.rope_sin, (uint32_t)L.qf, L.NQT, p.Tv, NL, p.Lmax, p.Lp, l, 0};
+        gx.W = p.w1 + (size_t)l * 2560 * D;
+        gemm_stage<4, 4>(gx, 2560, D, 1, e);
+      }
+      mark(p, 1, t0);
+      grid_sync(grid);
+      mark(p, 9, t0);
+      stage_att(p, ws, l);
+      mark(p, 2, t0);
+      grid_sync(grid);
+      mark(p, 9, t0);
+      stage_comb(p, ws);
+      mark(p, 3, t0);
+      grid_sync(grid);
+      mark(p, 9, t0);
+      {
+        EpiPart e{ws, (uint32_t)L.part, L.MP, 0};
+        ga.W = p.wo + (size_t)l * D * QD;
+        gemm_stage<4, 4>(ga, D, QD, KSPLIT, e);
+      }
+      mark(p, 4, t0);
+      grid_sync(grid);
+      mark(p, 9, t0);
+      stage_norm<1>(p, ws, xtr, mod_in + 2 * D, mod_post, mod_post + D, 0.f);
+      mark(p, 5, t0);
+      grid_sync(grid);
+      mark(p, 9, t0);
+      {
+        EpiGelu e{ws, (uint32_t)L.h, 0};
+        gx.W = p.w2 + (size_t)l * 8192 * D;
+        gemm_stage<4, 8>(gx, 8192, D, 1, e);
+      }
+      mark(p, 6, t0);
+      grid_sync(grid);
+      mark(p, 9, t0);
+      {
+        EpiPart e{ws, (uint32_t)L.part, L.MP, 0};
+        gh.W = p.w3 + (size_t)l * D * FF;
+        gemm_stage<4, 4>(gh, D, FF, KSPLIT, e);
+      }
+      mark(p, 7, t0);
+      grid_sync(grid);
+      mark(p, 9, t0);
+    }
+    const int li = step * NL + NL - 1;
+    const float* gl = p.mods + ((size_t)li * 2 + 1) * 3 * D + 2 * D;
+    const float* mf = p.mod_final + (size_t)step * 3 * D;
+    stage_norm<2>(p, ws, xtr, gl, mf, mf + D, dt);
+    mark(p, 8, t0);
+    grid_sync(grid);  // x_t of every token is final before the next step's embed reads it
+    mark(p, 9, t0);
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p.ws + OFF_CTRL), seq + 1, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace pb
+}  // namespace fa
+
+// ================================================================= host side
+namespace fa {
+
+// Batched launch of fa_pi05_denoise (batch >= 2); argument checks common to both paths are done
+// by the caller in pi05_bs1.hip.
+size_t pi05_batched_workspace_bytes(int batch, int Tv, int Lmax) {
+  if (batch < 1 || Tv < 1 || Lmax < 16) return 0;
+  if ((size_t)batch * Tv > (size_t)pb::MAX_TOKENS) return 0;
+  const size_t n = pb::layout(batch, Tv, Lmax).total;
+  return n < 0xffffffffull ? n : 0;
+}
+
+int pi05_denoise_batched(const fa_pi05_args* a, fa_stream_t stream) {
+  using namespace fa::pb;
+  if ((size_t)a->batch * a->Tv > (size_t)MAX_TOKENS)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: batch x Tv = %d exceeds %d tokens", a->batch * a->Tv,
+                      MAX_TOKENS);
+  const size_t need = pi05_batched_workspace_bytes(a->batch, a->Tv, a->Lmax);
+  if (need == 0 || a->workspace_bytes < need)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: workspace of %zu bytes, batch %d needs %zu",
+                      a->workspace_bytes, a->batch, need);
+  const size_t cache_bytes = (size_t)a->batch * a->num_layers * a->Lmax * HD * 2;
+  if (cache_bytes >= 0xffffffffull)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: caches of %zu bytes exceed the 4 GB buffer range",
+                      cache_bytes);
+  if (a->trace)
+    return host::fail(FA_ERR_UNSUPPORTED, "fa_pi05_denoise: per-wave traces exist for batch 1 only");
+  Params p;
+  p.w1 = static_cast<const bf16*>(a->w1);
+  p.wo = static_cast<const bf16*>(a->wo);
+  p.w2 = static_cast<const bf16*>(a->w2);
+  p.w3 = static_cast<const bf16*>(a->w3);
+  p.mods = a->mods;
+  p.mod_final = a->mod_final;
+  p.rope_cos = a->rope_cos;
+  p.rope_sin = a->rope_sin;
+  p.w_ain = a->w_ain;
+  p.b_ain = a->b_ain;
+  p.w_aout = a->w_aout;
+  p.b_aout = a->b_aout;
+  p.kcache = static_cast<bf16*>(a->kcache);
+  p.vtcache = static_cast<bf16*>(a->vtcache);
+  p.x_t = a->x_t;
+  p.stage_cycles = a->stage_cycles;
+  p.ws = static_cast<unsigned char*>(a->workspace);
+  p.L = layout(a->batch, a->Tv, a->Lmax);
+  p.NL = a->num_layers;
+  p.Lp = a->Lp;
+  p.Lmax = a->Lmax;
+  p.S = a->num_steps;
+  p.Tv = a->Tv;
+  p.B = a->batch;
+  p.xt_rows = a->xt_rows;
+  int rc = host::check_device((const void*)pb::pi05_batched_kernel, NTHR, LDS_BYTES, NWG, "fa_pi05_denoise");
+  if (rc != FA_OK) return rc;
+  void* args[] = {&p};
+  hipError_t e = hipLaunchCooperativeKernel((const void*)pb::pi05_batched_kernel, dim3(NWG), dim3(NTHR), args, LDS_BYTES,
+                                            (hipStream_t)stream);
+  if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_pi05_denoise: batched launch: %s", hipGetErrorString(e));
+  return FA_OK;
+}
+
+}  // namespace fa

@@ -995,13 +995,12 @@ __global__ void ws_zero(u32x4* p, size_t n16) {
 using namespace fa;
 
 extern "C" size_t fa_pi05_workspace_bytes(int batch, int Tv, int Lmax) {
-  (void)Tv;
-  (void)Lmax;
-  if (batch != 1) return 0;
-  return pi05::WS_BYTES;
+  if (batch == 1) return pi05::WS_BYTES;
+  if (batch < 1 || batch > fa_pi05_max_batch()) return 0;
+  return pi05_batched_workspace_bytes(batch, Tv, Lmax);
 }
 
-extern "C" int fa_pi05_max_batch(void) { return 1; }
+extern "C" int fa_pi05_max_batch(void) { return 64; }
 
 extern "C" int fa_pi05_workspace_init(void* workspace, size_t bytes, fa_stream_t stream) {
   if (!workspace || bytes == 0 || (bytes & 15) || (reinterpret_cast<uintptr_t>(workspace) & 255))
@@ -1031,8 +1030,8 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: fp8 row scales must be NULL for bf16 weights");
   if (a->srows != 0 || a->kvsrc_k || a->kvsrc_v)
     return host::fail(FA_ERR_UNSUPPORTED, "fa_pi05_denoise: the KV hand-off prologue (srows > 0) is not implemented");
-  if (a->batch != 1)
-    return host::fail(FA_ERR_UNSUPPORTED, "fa_pi05_denoise: batch=%d (this entry point runs batch 1)", a->batch);
+  if (a->batch < 1 || a->batch > fa_pi05_max_batch())
+    return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: batch=%d outside [1, %d]", a->batch, fa_pi05_max_batch());
   const void* ptrs[] = {a->w1, a->wo, a->w2, a->w3, a->mods, a->mod_final, a->rope_cos, a->rope_sin, a->w_ain,
                         a->b_ain, a->w_aout, a->b_aout, a->kcache, a->vtcache, a->x_t, a->workspace};
   const char* names[] = {"w1", "wo", "w2", "w3", "mods", "mod_final", "rope_cos", "rope_sin", "w_ain",
@@ -1056,6 +1055,7 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: KV cache larger than 2 GiB per sample");
   if (a->xt_rows < a->Tv)
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: xt_rows=%d < Tv=%d", a->xt_rows, a->Tv);
+  if (a->batch > 1) return pi05_denoise_batched(a, stream);
   if (a->workspace_bytes < WS_BYTES)
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: workspace_bytes=%zu < required %u", a->workspace_bytes,
                       (unsigned)WS_BYTES);

@@ -73,3 +73,20 @@ def parity(gpu_out: np.ndarray, ref: np.ndarray) -> dict:
     a, b = gpu_out.ravel().astype(np.float64), ref.ravel().astype(np.float64)
     cos = float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-30))
     return {"max_abs": float(d.max()), "mean_abs": float(d.mean()), "cos": cos}
+
+
+def run_gpu_batched(c, device, g=None, xt_rows=None):
+    """One batched launch over all samples; returns (x_t [B][Tv][32] numpy, kcache, vtcache)."""
+    g = g or gpu_tensors(c, device)
+    p = g["packed"]
+    kc = torch.stack([k for k, _ in g["caches"]]).contiguous()
+    vc = torch.stack([v for _, v in g["caches"]]).contiguous()
+    rows = xt_rows or c["Tv"]
+    x_t = torch.zeros(c["batch"], rows, 32, dtype=torch.float32, device=device)
+    x_t[:, :c["Tv"]] = c["inp"]["noise"].to(device)
+    empty = torch.empty(0, device=device)
+    pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], empty, empty, empty, empty, g["mods"], g["mod_final"],
+                g["cos"], g["sin"], g["w_ain"], g["b_ain"], g["w_aout"], g["b_aout"], None, None, 0,
+                kc, vc, c["Lp"], g["Lmax"], c["S"], c["Tv"], x_t)
+    torch.cuda.synchronize(device)
+    return x_t.cpu().numpy(), kc, vc

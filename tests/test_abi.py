@@ -67,7 +67,10 @@ def _args(**kw):
     (dict(kcache=(1 << 20) + 8), 1, "kcache is not 16-byte aligned"),
     (dict(srows=4), 2, "hand-off"),
     (dict(weight_dtype=1), 2, "bf16"),
-    (dict(batch=3), 2, "batch"),
+    (dict(batch=65), 1, "batch"),
+    (dict(batch=0), 1, "batch"),
+    (dict(batch=16, workspace_bytes=4096), 1, "workspace"),
+    (dict(batch=16, trace=1 << 20), 2, "batch 1"),
 ])
 def test_denoise_rejects_bad_requests(lib, kw, code, text):
     rc = lib.fa_pi05_denoise(ctypes.byref(_args(**kw)), None)
@@ -86,3 +89,14 @@ def test_denoise_without_device(lib):
     if torch.cuda.is_available():
         pytest.skip("a GPU is present")
     assert lib.fa_pi05_denoise(ctypes.byref(_args()), None) == 3
+    assert lib.fa_pi05_denoise(ctypes.byref(_args(batch=16)), None) == 3
+
+
+def test_batched_workspace_sizes(lib):
+    """bs >= 2 selects the batched kernel: its workspace grows with batch x Tv and the key range."""
+    one = lib.fa_pi05_workspace_bytes(1, 50, 1024)
+    b2 = lib.fa_pi05_workspace_bytes(2, 50, 1024)
+    b16 = lib.fa_pi05_workspace_bytes(16, 50, 1024)
+    assert 0 < b2 < b16 and b16 % 256 == 0 and one > 0
+    assert lib.fa_pi05_workspace_bytes(16, 50, 2048) > b16
+    assert lib.fa_pi05_workspace_bytes(lib.fa_pi05_max_batch() + 1, 50, 1024) == 0

@@ -6,7 +6,9 @@ as ONE cooperative kernel launch. Inputs are seeded synthetic tensors already re
 
 Prints one JSON line: value = ms per chunk (lower is better), the roofline of the kernel
 (algorithmic bytes / measured launch time vs 8 TB/s), the CPU fp32 oracle timed on the host
-cores (cpu_baseline), and the parity of the first GPU chunk vs that oracle run.
+cores (cpu_baseline), the parity of the first GPU chunk vs that oracle run, and "bs16": the
+metric's second half, chunks/s of the batch-16 launch and its MFMA
+utilisation (algorithmic FLOPs / launch time vs 2.5 PFLOP/s dense bf16).
 """
 from __future__ import annotations
 
@@ -27,6 +29,7 @@ from flashact_amd import pi05, synthetic  # noqa: E402
 NL, D, HD, F, AD = 18, 1024, 256, 4096, 32
 LP, TV, S = 968, 50, 10
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 # L2 <-> memory bytes of one pi05_denoise_bs1 launch at this workload, from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE passes scaled by a 1 GiB device copy (profiles/pi05_denoise_bs1_traffic.md). Counters
 # cannot be read inside a timed run, so the figure is the last measured one for this kernel.
@@ -43,6 +46,58 @@ def algorithmic_bytes_per_chunk(nl=NL, lp=LP, tv=TV, s=S) -> int:
     mods = (2 * nl + 1) * 3 * D * 4
     action_io = (D * AD + D + AD * D + AD) * 4
     return s * (weights + prefix_kv + suffix_kv + mods + action_io)
+
+
+def flops_per_launch(batch, nl=NL, lp=LP, tv=TV, s=S) -> int:
+    """Algorithmic FLOPs of one launch: 2 x tokens x expert parameters (projections), QK^T and PV
+    over Lp + Tv keys for 8 heads of every sample, action in/out projections; times the steps."""
+    params_per_layer = (2560 * D) + (D * 2048) + (8192 * D) + (D * F)
+    m = batch * tv
+    proj = 2 * m * params_per_layer * nl
+    attn = batch * nl * 8 * tv * (lp + tv) * HD * 2 * 2
+    action_io = 2 * m * (AD * D) * 2
+    return s * (proj + attn + action_io)
+
+
+def bench_batched(dev, batch, steps, warmup, seed=0):
+    """the batched launch (batch samples, each with its own prefix KV and noise)."""
+    w = synthetic.pi05_weights(seed, dev, NL=NL)
+    inp = synthetic.pi05_inputs(seed + 1, dev, batch=batch, NL=NL, Lp=LP, Tv=TV)
+    mods, modf = pi05.precompute_mods(S, w["w_ti"], w["b_ti"], w["w_to"], w["b_to"], w["w_in"], w["b_in"],
+                                      w["w_post"], w["b_post"], w["w_fin"], w["b_fin"])
+    packed = pi05.pack_weights(w["wq"], w["wk"], w["wv"], w["wo"], w["wg"], w["wu"], w["wd"])
+    cos, sin = pi05.rope_table(LP, TV, device=dev)
+    Lmax = pi05.lmax_for(LP, TV)
+    caches = [pi05.make_caches(torch.stack([inp["kpre"][b], inp["vpre"][b]], dim=1), Lmax) for b in range(batch)]
+    kc = torch.stack([c[0] for c in caches]).contiguous()
+    vc = torch.stack([c[1] for c in caches]).contiguous()
+    del caches, inp["kpre"], inp["vpre"]
+    x_t = inp["noise"].clone()
+    empty = torch.empty(0, device=dev)
+
+    def launch():
+        pi05.launch(packed["w1"], packed["wo"], packed["w2"], packed["w3"], empty, empty, empty, empty, mods, modf,
+                    cos, sin, w["w_ain"], w["b_ain"], w["w_aout"], w["b_aout"], None, None, 0, kc, vc, LP, Lmax,
+                    S, TV, x_t)
+
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    fl = flops_per_launch(batch)
+    tflops = fl / (ms * 1e-3) / 1e12
+    status = pi05.read_status(pi05.workspace(dev, batch, TV, Lmax))
+    return {"workload": f"pi05_expert_bs{batch}_T50_Lp968_S10", "batch": batch, "chunks_per_s": round(batch / ms * 1e3, 1),
+            "ms_per_launch": round(ms, 3), "launches": steps, "warmup": warmup, "flops_per_launch": fl,
+            "achieved_tflops": round(tflops, 1), "mfma_peak_tflops": MFMA_PEAK_TFLOPS,
+            "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "kernel_status": status}
 
 
 def build_inputs(dev, seed=0):
@@ -85,6 +140,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline and parity check")
+    ap.add_argument("--bs16-launches", type=int, default=10,
+                    help="timed launches of the batch-16 kernel (BASELINE config 2); 0 skips it")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="first run a plain device copy of this many bytes (twice), the calibration dispatch for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
@@ -157,6 +214,8 @@ def main():
         "wall_ms_per_step": round(t_wall * 1000.0 / args.steps, 4),
         "kernel_status": status,
     }
+    if args.bs16_launches > 0:
+        res["bs16"] = bench_batched(dev, 16, args.bs16_launches, 2)
     if not args.no_cpu:
         cpu_ms, ref, threads = cpu_baseline(w, inp, mods, modf, cos, sin)
         d = np.abs(first[:TV].astype(np.float64) - ref[0].astype(np.float64))

@@ -190,14 +190,30 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
     }
   }
   __syncthreads();  // the ring is free for the next tile
+  // Epilogue inputs (e.g. RoPE factors) are fetched for every block before the first store, so
+  // the loads are not serialised behind stores the compiler must assume may alias them.
+  typename Epi::Pre pre[WN][WM];
 #pragma unroll
   for (int j = 0; j < WN; j++)
 #pragma unroll
     for (int i = 0; i < WM; i++) {
       const int m = m0 + 16 * (wm * WM + i) + lr;
-      if (m < g.M) epi(n0 + 16 * (wn * WN + j) + 4 * lq, m, acc[j][i]);
+      pre[j][i] = epi.pre(n0 + 16 * (wn * WN + j) + 4 * lq, m < g.M ? m : 0);
+    }
+#pragma unroll
+  for (int j = 0; j < WN; j++)
+#pragma unroll
+    for (int i = 0; i < WM; i++) {
+      const int m = m0 + 16 * (wm * WM + i) + lr;
+      if (m < g.M) epi(n0 + 16 * (wn * WN + j) + 4 * lq, m, acc[j][i], pre[j][i]);
     }
 }
+
+// Epilogue base for epilogues without per-element inputs.
+struct NoPre {
+  struct Pre {};
+  __device__ Pre pre(int, int) const { return Pre{}; }
+};
 
 // Runs every tile of an [M x N] GEMM, K split into `ksplit` equal ranges (multiples of 64). Items
 // are ordered m-tile fastest so the items of one weight tile run on neighbouring CUs of one XCD.

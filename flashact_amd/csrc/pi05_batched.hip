@@ -97,7 +97,15 @@ struct EpiQKV {  // RoPE on q/k pairs (rows 2p, 2p+1 = dims j, j+128), q -> Qf, 
   const float* rsin;
   uint32_t qf;
   int NQT, Tv, NL, Lmax, Lp, l, split;
-  __device__ void operator()(int n0, int m, f32x4 v) const {
+  typedef f32x4 Pre;  // cos j0, cos j0+1, sin j0, sin j0+1 of the lane's token
+  __device__ Pre pre(int n0, int m) const {
+    if (n0 >= 2304) return f32x4{0.f, 0.f, 0.f, 0.f};
+    const int t = m % Tv, j0 = ((n0 < 2048 ? n0 : n0 - 2048) >> 1) & 127;
+    const f32x2 c = *reinterpret_cast<const f32x2*>(rcos + t * 128 + j0);
+    const f32x2 sn = *reinterpret_cast<const f32x2*>(rsin + t * 128 + j0);
+    return f32x4{c[0], c[1], sn[0], sn[1]};
+  }
+  __device__ void operator()(int n0, int m, f32x4 v, f32x4 cs) const {
     const int b = m / Tv, t = m - b * Tv;
     if (n0 >= 2304) {  // v rows: dims n0-2304 .. +3 of key Lp+t
       const int d0 = n0 - 2304;
@@ -108,10 +116,8 @@ struct EpiQKV {  // RoPE on q/k pairs (rows 2p, 2p+1 = dims j, j+128), q -> Qf, 
     }
     const int p0 = (n0 < 2048 ? n0 : n0 - 2048) >> 1;  // first of two RoPE pairs
     const int j0 = p0 & 127;
-    const float c0 = rcos[t * 128 + j0], c1 = rcos[t * 128 + j0 + 1];
-    const float s0 = rsin[t * 128 + j0], s1 = rsin[t * 128 + j0 + 1];
-    const float lo0 = v[0] * c0 - v[1] * s0, hi0 = v[1] * c0 + v[0] * s0;
-    const float lo1 = v[2] * c1 - v[3] * s1, hi1 = v[3] * c1 + v[2] * s1;
+    const float lo0 = v[0] * cs[0] - v[1] * cs[2], hi0 = v[1] * cs[0] + v[0] * cs[2];
+    const float lo1 = v[2] * cs[1] - v[3] * cs[3], hi1 = v[3] * cs[1] + v[2] * cs[3];
     const unsigned plo = pack_bf16x2(lo0, lo1), phi = pack_bf16x2(hi0, hi1);
     if (n0 < 2048) {
       const int r = (p0 >> 7) * Tv + t;
@@ -125,21 +131,21 @@ struct EpiQKV {  // RoPE on q/k pairs (rows 2p, 2p+1 = dims j, j+128), q -> Qf, 
   }
 };
 
-struct EpiGelu {  // rows 2f, 2f+1 = gate f, up f -> h[m][f] = gelu_tanh(g) u
+struct EpiGelu : NoPre {  // rows 2f, 2f+1 = gate f, up f -> h[m][f] = gelu_tanh(g) u
   rsrc_t ws;
   uint32_t off;
   int split;
-  __device__ void operator()(int n0, int m, f32x4 v) const {
+  __device__ void operator()(int n0, int m, f32x4 v, Pre) const {
     const unsigned pk = pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]);
     st_b32(ws, off + (uint32_t)(((size_t)m * FF + (n0 >> 1)) * 2), pk);
   }
 };
 
-struct EpiPart {  // fp32 partial sums [split][MP][1024]
+struct EpiPart : NoPre {  // fp32 partial sums [split][MP][1024]
   rsrc_t ws;
   uint32_t off;
   int MP, split;
-  __device__ void operator()(int n0, int m, f32x4 v) const {
+  __device__ void operator()(int n0, int m, f32x4 v, Pre) const {
     st_b128(ws, off + (uint32_t)((((size_t)split * MP + m) * D + n0) * 4), as_u32x4(v));
   }
 };
@@ -251,7 +257,7 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
 
 // ---------------------------------------------------------------- attention partials
 // Item (b, kc, qg): keys [128 kc, 128 kc + 128) of sample b against query tiles 16 qg + w + 4 j
-// (wave w, j < 4, processed one after the other). The chunk's K rows and V^T columns are copied
+// (wave w, j < 4, two tiles per pass). The chunk's K rows and V^T columns are copied
 // to LDS once, in MFMA fragment order (64 + 64 fragments). K rows are permuted inside each 32-key
 // span so that the S^T accumulators of key tiles (2 sp, 2 sp + 1) are directly the P^T operand of
 // k-step sp: tile row 4a + i of key tile 2 sp + kt holds key 32 sp + 8 a + 4 kt + i.
@@ -297,110 +303,168 @@ __device__ __forceinline__ void stage_att(const Params& p, rsrc_t ws, int l) {
     }
     vm_wait<0>();
     __syncthreads();
+    // two query tiles per pass (qt, qt + 4): every K / V^T fragment read from LDS feeds 2 MFMAs
 #pragma unroll 1
-    for (int j = 0; j < QTG / 4; j++) {
-      const int qt = QTG * qg + w + 4 * j;
-      if (qt >= L.NQT) break;
-      u32x4 qf[8];
+    for (int jp = 0; jp < QTG / 8; jp++) {
+      const int qt[2] = {QTG * qg + w + 8 * jp, QTG * qg + w + 8 * jp + 4};
+      if (qt[0] >= L.NQT) break;
+      const bool has1 = qt[1] < L.NQT;
+      u32x4 qf[2][8];
 #pragma unroll
-      for (int ks = 0; ks < 8; ks++)
-        qf[ks] = ldb128<kCpSc1>(ws, (uint32_t)(L.qf + ((((size_t)b * L.NQT + qt) * 8 + ks) * 64 + lane) * 16));
-      f32x4 s[8];
+      for (int q = 0; q < 2; q++) {
+        const int tq = (q == 1 && !has1) ? qt[0] : qt[q];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+          qf[q][ks] = ldb128<kCpSc1>(ws, (uint32_t)(L.qf + ((((size_t)b * L.NQT + tq) * 8 + ks) * 64 + lane) * 16));
+      }
+      f32x4 s[2][8];
 #pragma unroll
       for (int kt8 = 0; kt8 < 8; kt8++) {
-        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+        f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) a = mfma16(lds128((kt8 * 8 + ks) * 1024 + lane * 16), qf[ks], a);
-        s[kt8] = a;
-      }
-      float mx = -1e30f;
-#pragma unroll
-      for (int kt8 = 0; kt8 < 8; kt8++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int key = key0 + 32 * (kt8 >> 1) + 8 * lq + 4 * (kt8 & 1) + i;
-          s[kt8][i] = key < kend ? s[kt8][i] * qscale : -1e30f;
-          mx = fmaxf(mx, s[kt8][i]);
+        for (int ks = 0; ks < 8; ks++) {
+          const u32x4 kf = lds128((kt8 * 8 + ks) * 1024 + lane * 16);
+          a0 = mfma16(kf, qf[0][ks], a0);
+          a1 = mfma16(kf, qf[1][ks], a1);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      float psum = 0.f;
-      u32x4 pb[4];
+        s[0][kt8] = a0;
+        s[1][kt8] = a1;
+      }
+      float mx[2], psum[2];
+      u32x4 pb[2][4];
 #pragma unroll
-      for (int sp = 0; sp < 4; sp++) {
-        float pv[8];
+      for (int q = 0; q < 2; q++) {
+        float m_ = -1e30f;
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++)
+        for (int kt8 = 0; kt8 < 8; kt8++)
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            pv[4 * kt + i] = exp2f(s[2 * sp + kt][i] - mx);
-            psum += pv[4 * kt + i];
+            const int key = key0 + 32 * (kt8 >> 1) + 8 * lq + 4 * (kt8 & 1) + i;
+            s[q][kt8][i] = key < kend ? s[q][kt8][i] * qscale : -1e30f;
+            m_ = fmaxf(m_, s[q][kt8][i]);
           }
-        pb[sp] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
-                       pack_bf16x2(pv[6], pv[7])};
+        m_ = fmaxf(m_, __shfl_xor(m_, 16, 64));
+        m_ = fmaxf(m_, __shfl_xor(m_, 32, 64));
+        float ps = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < 4; sp++) {
+          float pv[8];
+#pragma unroll
+          for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              pv[4 * kt + i] = exp2f(s[q][2 * sp + kt][i] - m_);
+              ps += pv[4 * kt + i];
+            }
+          pb[q][sp] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                            pack_bf16x2(pv[6], pv[7])};
+        }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        mx[q] = m_;
+        psum[q] = ps;
       }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
-      f32x4 o[16];
+      // O^T = V^T P^T, one 16-dim tile at a time, stored as soon as it is complete: lane holds
+      // O^T[dim 16 dt + 4 lq + i][query row 16 qt + lr]
+      bool st[2];
+      size_t prow[2];
+      float inv[2];
+#pragma unroll
+      for (int q = 0; q < 2; q++) {
+        const int r = 16 * qt[q] + lr;
+        st[q] = (q == 0 || has1) && r < NH * p.Tv;
+        prow[q] = ((size_t)b * L.NKC + kc) * L.NQT * 16 + r;
+        inv[q] = 1.0f / psum[q];
+      }
 #pragma unroll
       for (int dt = 0; dt < 16; dt++) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int sp = 0; sp < 4; sp++) {
           u32x4 va = lds128((64 + dt * 4 + sp) * 1024 + lane * 16);
 #pragma unroll
           for (int e = 0; e < 4; e++) va[e] &= vmask[sp][e];
-          acc = mfma16(va, pb[sp], acc);
+          o0 = mfma16(va, pb[0][sp], o0);
+          o1 = mfma16(va, pb[1][sp], o1);
         }
-        o[dt] = acc;
+        if (st[0])
+          st_b64(ws, (uint32_t)(L.attp + (prow[0] * HD + 16 * dt + 4 * lq) * 2),
+                 u32x2{pack_bf16x2(o0[0] * inv[0], o0[1] * inv[0]), pack_bf16x2(o0[2] * inv[0], o0[3] * inv[0])});
+        if (st[1])
+          st_b64(ws, (uint32_t)(L.attp + (prow[1] * HD + 16 * dt + 4 * lq) * 2),
+                 u32x2{pack_bf16x2(o1[0] * inv[1], o1[1] * inv[1]), pack_bf16x2(o1[2] * inv[1], o1[3] * inv[1])});
       }
-      // lane holds O^T[dim 16 dt + 4 lq + i][query row 16 qt + lr]
-      const int r = 16 * qt + lr;
-      if (r < NH * p.Tv) {
-        const float inv = 1.0f / psum;
-        const size_t prow = ((size_t)b * L.NKC + kc) * L.NQT * 16 + r;
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++)
-          st_b64(ws, (uint32_t)(L.attp + (prow * HD + 16 * dt + 4 * lq) * 2),
-                 u32x2{pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv), pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv)});
-        if (lq == 0) st_b64(ws, (uint32_t)(L.ml + prow * 8), u32x2{as_u32(mx), as_u32(psum)});
-      }
+      for (int q = 0; q < 2; q++)
+        if (st[q] && lq == 0) st_b64(ws, (uint32_t)(L.ml + prow[q] * 8), u32x2{as_u32(mx[q]), as_u32(psum[q])});
     }
   }
 }
 
 // ---------------------------------------------------------------- combine
-// One wave per (sample, query row): attn[b Tv + t][256 h + d] = sum_c w_c O_c, w_c ~ l_c 2^(m_c - M).
+// attn[b Tv + t][256 h + d] = sum_c w_c O_c with w_c = l_c 2^(m_c - M) / sum. A wave combines 4
+// query rows at once (16 lanes per row, 16 dims per lane); the (m, l) pairs and the partials of up
+// to 8 chunks are all in flight together.
 __device__ __forceinline__ void stage_comb(const Params& p, rsrc_t ws) {
   const Layout& L = p.L;
-  const int lane = lane_id();
+  const int lane = lane_id(), sub = lane >> 4, l16 = lane & 15;
   const int Ltot = p.Lp + p.Tv, nkc = (Ltot + KCH - 1) / KCH;
   const int rows = p.B * NH * p.Tv;
 #pragma unroll 1
-  for (int R = vwg() * 4 + wave_id(); R < rows; R += NWG * 4) {
-    const int b = R / (NH * p.Tv), r = R - b * NH * p.Tv, h = r / p.Tv, t = r - h * p.Tv;
-    float mc = -1e30f, lc = 0.f;
-    if (lane < nkc) {
-      const u32x2 ml = ldb64<kCpSc1>(ws, (uint32_t)(L.ml + ((((size_t)b * L.NKC + lane) * L.NQT * 16) + r) * 8));
-      mc = as_f32(ml[0]);
-      lc = as_f32(ml[1]);
-    }
-    const float Mx = wave_max(mc);
-    const float wgt = lc * exp2f(mc - Mx);
-    const float wn = wgt / wave_sum(wgt);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int R0 = (vwg() * 4 + wave_id()) * 4; R0 < rows; R0 += NWG * 16) {
+    const int R = R0 + sub;
+    const bool valid = R < rows;
+    const int Rc = valid ? R : R0;
+    const int b = Rc / (NH * p.Tv), r = Rc - b * NH * p.Tv, h = r / p.Tv, t = r - h * p.Tv;
+    const size_t cstride = (size_t)L.NQT * 16;  // rows per chunk
+    const size_t row0 = (size_t)b * L.NKC * cstride + r;
+    float Mx = -1e30f, den = 0.f;
+    f32x4 acc[4] = {};
 #pragma unroll 1
-    for (int c = 0; c < nkc; c++) {
-      const float wc = __shfl(wn, c, 64);
-      const u32x2 v = ldb64<kCpSc1>(ws, (uint32_t)(L.attp + ((((size_t)b * L.NKC + c) * L.NQT * 16 + r) * HD + 4 * lane) * 2));
-      acc[0] = fmaf(wc, bf_lo(v[0]), acc[0]);
-      acc[1] = fmaf(wc, bf_hi(v[0]), acc[1]);
-      acc[2] = fmaf(wc, bf_lo(v[1]), acc[2]);
-      acc[3] = fmaf(wc, bf_hi(v[1]), acc[3]);
+    for (int c0 = 0; c0 < nkc; c0 += 8) {
+      u32x2 ml[8];
+      u32x4 v[8][2];
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        const bool ok = c0 + c < nkc;
+        const size_t prow = row0 + (size_t)(c0 + c) * cstride;
+        ml[c] = ldb64<kCpSc1>(ws, ok ? (uint32_t)(L.ml + prow * 8) : (uint32_t)L.ml);
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+          v[c][k] = ldb128<kCpSc1>(ws, ok ? (uint32_t)(L.attp + (prow * HD + 16 * l16 + 8 * k) * 2) : (uint32_t)L.attp);
+      }
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        if (c0 + c >= nkc) break;
+        const float mc = as_f32(ml[c][0]), lc = as_f32(ml[c][1]);
+        const float mn = fmaxf(Mx, mc);
+        const float sa = exp2f(Mx - mn), sc = lc * exp2f(mc - mn);
+        Mx = mn;
+        den = den * sa + sc;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+#pragma unroll
+          for (int e = 0; e < 2; e++) {
+            acc[2 * k + e][0] = acc[2 * k + e][0] * sa + sc * bf_lo(v[c][k][2 * e]);
+            acc[2 * k + e][1] = acc[2 * k + e][1] * sa + sc * bf_hi(v[c][k][2 * e]);
+            acc[2 * k + e][2] = acc[2 * k + e][2] * sa + sc * bf_lo(v[c][k][2 * e + 1]);
+            acc[2 * k + e][3] = acc[2 * k + e][3] * sa + sc * bf_hi(v[c][k][2 * e + 1]);
+          }
+        }
+      }
     }
-    const int m = b * p.Tv + t;
-    st_b64(ws, (uint32_t)(L.attn + ((size_t)m * QD + h * HD + 4 * lane) * 2),
-           u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])});
+    if (valid) {
+      const float inv = 1.0f / den;
+      const int m = b * p.Tv + t;
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const u32x4 o = {pack_bf16x2(acc[2 * k][0] * inv, acc[2 * k][1] * inv),
+                         pack_bf16x2(acc[2 * k][2] * inv, acc[2 * k][3] * inv),
+                         pack_bf16x2(acc[2 * k + 1][0] * inv, acc[2 * k + 1][1] * inv),
+                         pack_bf16x2(acc[2 * k + 1][2] * inv, acc[2 * k + 1][3] * inv)};
+        st_b128(ws, (uint32_t)(L.attn + ((size_t)m * QD + h * HD + 16 * l16 + 8 * k) * 2), o);
+      }
+    }
   }
 }
 
@@ -465,7 +529,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       grid_sync(grid);
       mark(p, 9, t0);
       {
-        EpiPart e{ws, (uint32_t)L.part, L.MP, 0};
+        EpiPart e{{}, ws, (uint32_t)L.part, L.MP, 0};
         ga.W = p.wo + (size_t)l * D * QD;
         gemm_stage<4, 4>(ga, D, QD, KSPLIT, e);
       }
@@ -477,7 +541,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       grid_sync(grid);
       mark(p, 9, t0);
       {
-        EpiGelu e{ws, (uint32_t)L.h, 0};
+        EpiGelu e{{}, ws, (uint32_t)L.h, 0};
         gx.W = p.w2 + (size_t)l * 8192 * D;
         gemm_stage<4, 8>(gx, 8192, D, 1, e);
       }
@@ -485,7 +549,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       grid_sync(grid);
       mark(p, 9, t0);
       {
-        EpiPart e{ws, (uint32_t)L.part, L.MP, 0};
+        EpiPart e{{}, ws, (uint32_t)L.part, L.MP, 0};
         gh.W = p.w3 + (size_t)l * D * FF;
         gemm_stage<4, 4>(gh, D, FF, KSPLIT, e);
       }

@@ -42,6 +42,25 @@ class Pi05Args(ctypes.Structure):
     ]
 
 
+class Ma2Args(ctypes.Structure):
+    _fields_ = [
+        ("weight_dtype", ctypes.c_int),
+        ("w_qkv", ctypes.c_void_p), ("w_so", ctypes.c_void_p), ("w_cq", ctypes.c_void_p), ("w_co", ctypes.c_void_p),
+        ("w_gu", ctypes.c_void_p), ("w_dn", ctypes.c_void_p),
+        ("b_qkv", ctypes.c_void_p), ("b_so", ctypes.c_void_p), ("b_cq", ctypes.c_void_p), ("b_co", ctypes.c_void_p),
+        ("b_gu", ctypes.c_void_p), ("b_dn", ctypes.c_void_p),
+        ("mods", ctypes.c_void_p), ("mod_final", ctypes.c_void_p),
+        ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p),
+        ("w_ain", ctypes.c_void_p), ("b_ain", ctypes.c_void_p), ("w_aout", ctypes.c_void_p), ("b_aout", ctypes.c_void_p),
+        ("kctx", ctypes.c_void_p), ("vtctx", ctypes.c_void_p),
+        ("Lk", ctypes.c_int), ("Lkmax", ctypes.c_int), ("Tv", ctypes.c_int), ("adim", ctypes.c_int),
+        ("num_steps", ctypes.c_int), ("num_layers", ctypes.c_int), ("batch", ctypes.c_int),
+        ("x_t", ctypes.c_void_p), ("xt_rows", ctypes.c_int),
+        ("stage_cycles", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class DeviceInfo(ctypes.Structure):
     _fields_ = [("cus", ctypes.c_int), ("xcds", ctypes.c_int), ("lds_bytes", ctypes.c_int),
                 ("coop_launch", ctypes.c_int), ("coop_max_blocks", ctypes.c_int), ("arch", ctypes.c_char * 64)]
@@ -54,6 +73,11 @@ SYMBOLS = [
     ("fa_pi05_workspace_init", ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     ("fa_pi05_read_status", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint)]),
     ("fa_pi05_max_batch", ctypes.c_int, []),
+    ("fa_ma2_flow", ctypes.c_int, [ctypes.POINTER(Ma2Args), ctypes.c_void_p]),
+    ("fa_ma2_workspace_bytes", ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    ("fa_ma2_workspace_init", ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    ("fa_ma2_read_status", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint)]),
+    ("fa_ma2_max_batch", ctypes.c_int, []),
     ("fa_device_query", ctypes.c_int, [ctypes.c_int, ctypes.POINTER(DeviceInfo)]),
     ("fa_last_error", ctypes.c_char_p, []),
     ("fa_abi_version", ctypes.c_int, []),

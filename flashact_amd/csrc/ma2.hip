@@ -1,0 +1,773 @@
+// MolmoAct2 action-expert flow loop (src/molmoact2/mk_ma2.cu:258-575): the whole S-step Euler
+// loop for a batch of samples in ONE cooperative launch of 256 workgroups x 4 waves, built on the
+// stage engine (engine.h). D = 768, 8 heads of 96, F = 3072, action dim 32 (the first `adim`
+// dims integrated), t_s = s / S, dt = +1/S.
+//
+// Per layer (grid barrier after each stage), token m = b * Tv + t of sample b:
+//   N_msa  x = embed(x_t) (layer 0) or x += g_mlp * (sum of down partials + b_dn); h = adaRMS(x)
+//   QKV    [M x 2304] = h W_qkv^T, K split -> fp32 partials
+//   SATT   per (sample, head): sum partials + b_qkv, per-head RMS of q and k, RoPE (split-half
+//          pairs d, d+48 at position t), softmax(q k^T / sqrt(96)) v over the Tv action tokens
+//   SO     [M x 768] = attn W_so^T -> partials
+//   N_mca  x += g_msa * (sum + b_so); h = adaRMS(x)
+//   CQ     [M x 768] = h W_cq^T -> partials
+//   CATT   per (sample, head, 128-key chunk): q = RMS(sum + b_cq), attention over the context
+//          keys (kctx rows, vtctx columns of head h) -> normalised partial O + (m, l)
+//   COMB   combine of the key chunks -> attn
+//   CO     [M x 768] = attn W_co^T -> partials
+//   N_mlp  x += g_mca * (sum + b_co); h = adaRMS(x)
+//   GU     [M x 6144] = h W_gu^T (rows 2f / 2f+1 = gate f / up f) -> partials
+//   GATE   m = silu(g + b_g) * (u + b_u) -> bf16
+//   DN     [M x 768] = m W_dn^T -> partials
+// then the final norm, action projection and Euler update of x_t[:, :adim].
+#include "engine.h"
+#include "../../include/flashact_mi355x.h"
+#include "fa_host.h"
+
+namespace fa {
+namespace ma2 {
+using namespace fa::eng;
+
+constexpr int D = 768, NH = 8, HD = 96, FF = 3072, AD = 32, QKVN = 3 * D, GUN = 2 * FF;
+constexpr int KCH = 128;  // context keys per cross-attention item
+constexpr int MAX_TV = 64;
+constexpr int MAX_TOKENS = 2048;
+constexpr int MAX_KS = 16;
+
+struct Layout {
+  int B, Tv, M, MP, NKC;
+  int ks_qkv, ks_d, ks_gu, ks_dn;  // K splits of QKV, the D x D projections, gate/up, down
+  size_t x, xn, attn, h, pqkv, pq, pgu, part, cattp, cml, total;
+};
+
+// K split for an [nm x N/BN] tile grid over K: the largest divisor of the 64-wide k-steps that
+// keeps the item count within one pass of the 256 workgroups.
+__host__ __device__ inline int pick_ks(int nm, int nn, int K) {
+  const int steps = K / 64;
+  int best = 1;
+  for (int ks = 1; ks <= steps && ks <= MAX_KS; ks++)
+    if (steps % ks == 0 && nm * nn * ks <= NWG) best = ks;
+  return best;
+}
+
+__host__ __device__ inline Layout layout(int B, int Tv, int Lkmax, int BM, int BN) {
+  Layout L;
+  L.B = B;
+  L.Tv = Tv;
+  L.M = B * Tv;
+  L.MP = (L.M + BM - 1) / BM * BM;
+  L.NKC = (Lkmax + KCH - 1) / KCH;
+  const int nm = L.MP / BM;
+  L.ks_qkv = pick_ks(nm, QKVN / BN, D);
+  L.ks_d = pick_ks(nm, D / BN, D);
+  L.ks_gu = pick_ks(nm, GUN / BN, D);
+  L.ks_dn = pick_ks(nm, D / BN, FF);
+  const int ks_part = L.ks_d > L.ks_dn ? L.ks_d : L.ks_dn;
+  size_t o = 4096;  // control block + 256 barrier slots
+  auto take = [&](size_t n) {
+    const size_t r = o;
+    o += (n + 255) / 256 * 256;
+    return r;
+  };
+  L.x = take((size_t)L.MP * D * 4);
+  L.xn = take((size_t)L.MP * D * 2);
+  L.attn = take((size_t)L.MP * D * 2);
+  L.h = take((size_t)L.MP * FF * 2);
+  L.pqkv = take((size_t)L.ks_qkv * L.MP * QKVN * 4);
+  L.pq = take((size_t)L.ks_d * L.MP * D * 4);
+  L.pgu = take((size_t)L.ks_gu * L.MP * GUN * 4);
+  L.part = take((size_t)ks_part * L.MP * D * 4);
+  L.cattp = take((size_t)B * NH * L.NKC * MAX_TV * HD * 2);
+  L.cml = take((size_t)B * NH * L.NKC * MAX_TV * 8);
+  L.total = o;
+  return L;
+}
+constexpr uint32_t OFF_CTRL = 0, OFF_FLAGS = 1024;
+
+struct Params {
+  const bf16 *w_qkv, *w_so, *w_cq, *w_co, *w_gu, *w_dn;
+  const float *b_qkv, *b_so, *b_cq, *b_co, *b_gu, *b_dn;
+  const float *mods, *mod_final, *rope_cos, *rope_sin, *w_ain, *b_ain;
+  const bf16* w_aout;
+  const float* b_aout;
+  const bf16* kctx;   // [B][NL][Lkmax][768]
+  const bf16* vtctx;  // [B][NL][768][Lkmax]
+  float* x_t;         // [B][xt_rows][32]
+  unsigned long long* stage_cycles;
+  unsigned char* ws;
+  Layout L;
+  int NL, Lk, Lkmax, Tv, adim, S, B, xt_rows;
+};
+
+struct EpiPartN : NoPre {  // fp32 partial sums [split][MP][N]
+  rsrc_t ws;
+  uint32_t off;
+  int MP, N, split;
+  __device__ void operator()(int n0, int m, f32x4 v, Pre) const {
+    st_b128(ws, off + (uint32_t)((((size_t)split * MP + m) * N + n0) * 4), as_u32x4(v));
+  }
+};
+
+// acc[q] += sum over the `ks` fp32 partial rows [s][MP][N] of row m, columns c[q]..c[q]+3; PB
+// partials (NC x PB 16-byte loads) are in flight per round trip.
+template <int NC, int PB>
+__device__ __forceinline__ void add_parts(rsrc_t ws, size_t base, int ks, int MP, int N, int m, const int (&c)[NC],
+                                          f32x4 (&acc)[NC]) {
+#pragma unroll 1
+  for (int s0 = 0; s0 < ks; s0 += PB) {
+    u32x4 v[PB][NC];
+#pragma unroll
+    for (int j = 0; j < PB; j++) {
+      const int sp = s0 + j < ks ? s0 + j : ks - 1;
+#pragma unroll
+      for (int q = 0; q < NC; q++) v[j][q] = ldb128<kCpSc1>(ws, (uint32_t)(base + (((size_t)sp * MP + m) * N + c[q]) * 4));
+    }
+#pragma unroll
+    for (int j = 0; j < PB; j++)
+      if (s0 + j < ks)
+#pragma unroll
+        for (int q = 0; q < NC; q++) acc[q] += as_f32x4(v[j][q]);
+  }
+}
+
+// ---------------------------------------------------------------- norm rows
+// One wave per token row; lane holds columns 4 lane + 256 k + i (k < 3). MODE 0: x = embed(x_t);
+// MODE 1: x += gate * (sum of partials + bias); MODE 2: as 1, then the final norm, the action
+// projection and the Euler update of x_t[:, :adim].
+template <int MODE>
+__device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xtr, int ks, const float* bias,
+                                           const float* gate, const float* scale, const float* shift, float dt) {
+  const Layout& L = p.L;
+  const int lane = lane_id();
+#pragma unroll 1
+  for (int m = vwg() * 4 + wave_id(); m < L.M; m += NWG * 4) {
+    const int b = m / p.Tv, t = m - b * p.Tv;
+    const uint32_t xto = (uint32_t)(((size_t)b * p.xt_rows + t) * AD * 4);
+    f32x4 x[3];
+    if (MODE == 0) {
+      const float xl = lane < AD ? ldbf32<kCpSc1>(xtr, xto + lane * 4) : 0.f;
+      float xa[AD];
+#pragma unroll
+      for (int a = 0; a < AD; a++) xa[a] = __shfl(xl, a, 64);
+#pragma unroll
+      for (int k = 0; k < 3; k++) {
+        const int d = 4 * lane + 256 * k;
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(p.b_ain + d);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          float s = bb[i];
+#pragma unroll
+          for (int q = 0; q < 8; q++) {
+            const f32x4 wv = *reinterpret_cast<const f32x4*>(p.w_ain + (d + i) * AD + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; e++) s = fmaf(wv[e], xa[4 * q + e], s);
+          }
+          x[k][i] = s;
+        }
+      }
+    } else {
+      u32x4 xo[3];
+      int cols[3];
+      f32x4 sum[3];
+#pragma unroll
+      for (int k = 0; k < 3; k++) {
+        cols[k] = 4 * lane + 256 * k;
+        xo[k] = ldb128<kCpSc1>(ws, (uint32_t)(L.x + ((size_t)m * D + cols[k]) * 4));
+        sum[k] = *reinterpret_cast<const f32x4*>(bias + cols[k]);
+      }
+      add_parts<3, 4>(ws, L.part, ks, L.MP, D, m, cols, sum);
+#pragma unroll
+      for (int k = 0; k < 3; k++) x[k] = as_f32x4(xo[k]) + *reinterpret_cast<const f32x4*>(gate + cols[k]) * sum[k];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 3; k++) ss += x[k][0] * x[k][0] + x[k][1] * x[k][1] + x[k][2] * x[k][2] + x[k][3] * x[k][3];
+    const float rr = rsqrtf(wave_sum(ss) / (float)D + 1e-6f);
+    f32x4 h[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+      const int d = 4 * lane + 256 * k;
+      const f32x4 sc = *reinterpret_cast<const f32x4*>(scale + d);
+      const f32x4 sh = *reinterpret_cast<const f32x4*>(shift + d);
+#pragma unroll
+      for (int i = 0; i < 4; i++) h[k][i] = x[k][i] * rr * (1.0f + sc[i]) + sh[i];
+    }
+    if (MODE != 2) {
+#pragma unroll
+      for (int k = 0; k < 3; k++) {
+        const int d = 4 * lane + 256 * k;
+        st_b128(ws, (uint32_t)(L.x + ((size_t)m * D + d) * 4), as_u32x4(x[k]));
+        st_b64(ws, (uint32_t)(L.xn + ((size_t)m * D + d) * 2),
+               u32x2{pack_bf16x2(h[k][0], h[k][1]), pack_bf16x2(h[k][2], h[k][3])});
+      }
+    } else {
+      float acc = 0.f;  // lane a < adim ends with v[a]
+#pragma unroll 1
+      for (int a = 0; a < p.adim; a++) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+          const u32x2 wv = *reinterpret_cast<const u32x2*>(p.w_aout + (size_t)a * D + 4 * lane + 256 * k);
+          s += bf_lo(wv[0]) * h[k][0] + bf_hi(wv[0]) * h[k][1] + bf_lo(wv[1]) * h[k][2] + bf_hi(wv[1]) * h[k][3];
+        }
+        s = wave_sum(s);
+        if (lane == a) acc = s;
+      }
+      if (lane < p.adim) {
+        const float xo = ldbf32<kCpSc1>(xtr, xto + lane * 4);
+        __builtin_amdgcn_raw_buffer_store_b32(as_u32(xo + dt * (acc + p.b_aout[lane])), xtr, xto + lane * 4, 0,
+                                              kCpSc1);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- gate/up activation
+// h[m][f] = silu(sum g + b_g) * (sum u + b_u); rows 2f / 2f+1 of the partials are gate f / up f.
+// Lane columns c = 4 lane + 256 k (g, u of f = c/2, c/2 + 1), 8 columns per round trip.
+__device__ __forceinline__ void stage_gate(const Params& p, rsrc_t ws, int l) {
+  const Layout& L = p.L;
+  const int lane = lane_id();
+  const float* bg = p.b_gu + (size_t)l * GUN;
+#pragma unroll 1
+  for (int m = vwg() * 4 + wave_id(); m < L.M; m += NWG * 4) {
+#pragma unroll 1
+    for (int k0 = 0; k0 < GUN / 256; k0 += 8) {
+      int cols[8];
+      f32x4 v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        cols[k] = 4 * lane + 256 * (k0 + k);
+        v[k] = *reinterpret_cast<const f32x4*>(bg + cols[k]);
+      }
+      add_parts<8, 2>(ws, L.pgu, L.ks_gu, L.MP, GUN, m, cols, v);
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        st_b32(ws, (uint32_t)(L.h + ((size_t)m * FF + (cols[k] >> 1)) * 2),
+               pack_bf16x2(silu(v[k][0]) * v[k][1], silu(v[k][2]) * v[k][3]));
+    }
+  }
+}
+
+// ---------------------------------------------------------------- attention pieces
+// LDS fragment layouts (1 KB per fragment, lane = row % 16 + 16 * ((k % 32) / 8), element k % 8):
+//   Q   (query tile qt, k-step ks)      rows = tokens
+//   K   (key tile kt, k-step ks)        row 4a + i of tile 2 sp + kt = key 32 sp + 8 a + 4 kt + i,
+//                                       so the S^T tiles (2 sp, 2 sp + 1) form the P^T operand of span sp
+//   V^T (dim tile dt, key span sp)      rows = dims, k = keys 32 sp .. 32 sp + 31 in order
+__device__ __forceinline__ uint32_t frag_pos(int row, int k) {
+  return (uint32_t)(((row & 15) + 16 * ((k & 31) >> 3)) * 16 + (k & 7) * 2);
+}
+__device__ __forceinline__ uint32_t kperm_row(int key) {  // key -> (tile * 16 + row) of the K layout
+  const int sp = key >> 5, o = key & 31;
+  return (uint32_t)((2 * sp + ((o & 7) >> 2)) * 16 + 4 * (o >> 3) + (o & 3));
+}
+
+// softmax(S^T) over NKT key tiles (keys 32 (kt/2) + 8 lq + 4 (kt%2) + i < kvalid), P^T operands,
+// then O^T = V^T P^T for the 6 dim tiles; returns (max, sum) and O^T (normalised by the sum).
+template <int NKT>
+__device__ __forceinline__ void attend(const u32x4 (&qf)[3], uint32_t kbase, uint32_t vbase, int kvalid,
+                                       const unsigned (&vmask)[NKT / 2][4], float& mx, float& psum, f32x4 (&o)[6]) {
+  const int lane = lane_id(), lq = lane >> 4;
+  const float qscale = 1.4426950408889634f * 0.10206207261596575f;  // log2(e) / sqrt(96)
+  f32x4 s[NKT];
+#pragma unroll
+  for (int kt = 0; kt < NKT; kt++) {
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 3; ks++) a = mfma16(lds128(kbase + (kt * 3 + ks) * 1024 + lane * 16), qf[ks], a);
+    s[kt] = a;
+  }
+  float m_ = -1e30f;
+#pragma unroll
+  for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int key = 32 * (kt >> 1) + 8 * lq + 4 * (kt & 1) + i;
+      s[kt][i] = key < kvalid ? s[kt][i] * qscale : -1e30f;
+      m_ = fmaxf(m_, s[kt][i]);
+    }
+  m_ = fmaxf(m_, __shfl_xor(m_, 16, 64));
+  m_ = fmaxf(m_, __shfl_xor(m_, 32, 64));
+  float ps = 0.f;
+  u32x4 pb[NKT / 2];
+#pragma unroll
+  for (int sp = 0; sp < NKT / 2; sp++) {
+    float pv[8];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        pv[4 * kt + i] = exp2f(s[2 * sp + kt][i] - m_);
+        ps += pv[4 * kt + i];
+      }
+    pb[sp] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                   pack_bf16x2(pv[6], pv[7])};
+  }
+  ps += __shfl_xor(ps, 16, 64);
+  ps += __shfl_xor(ps, 32, 64);
+  const float inv = 1.0f / ps;
+#pragma unroll
+  for (int dt = 0; dt < 6; dt++) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < NKT / 2; sp++) {
+      u32x4 va = lds128(vbase + (dt * (NKT / 2) + sp) * 1024 + lane * 16);
+#pragma unroll
+      for (int e = 0; e < 4; e++) va[e] &= vmask[sp][e];
+      acc = mfma16(va, pb[sp], acc);
+    }
+    o[dt] = acc * inv;
+  }
+  mx = m_;
+  psum = ps;
+}
+
+// Sum + bias of 24 consecutive columns of each of the NT column bases c0[i] (row m of the
+// [ks][MP][N] partials): v[i][24].
+template <int NT, int PB>
+__device__ __forceinline__ void load24(rsrc_t ws, size_t base, int ks, int MP, int N, int m, const int (&c0)[NT],
+                                       const float* const (&bias)[NT], float (&v)[NT][24]) {
+  int cols[6 * NT];
+  f32x4 acc[6 * NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int q = 0; q < 6; q++) {
+      cols[6 * t + q] = c0[t] + 4 * q;
+      acc[6 * t + q] = *reinterpret_cast<const f32x4*>(bias[t] + 4 * q);
+    }
+  add_parts<6 * NT, PB>(ws, base, ks, MP, N, m, cols, acc);
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int q = 0; q < 6; q++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[t][4 * q + i] = acc[6 * t + q][i];
+}
+
+// RMS over the 96 dims of a head held by 4 lanes (xor 16, 32) as 24 values each.
+__device__ __forceinline__ void rms96(float (&v)[24]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 24; i++) ss += v[i] * v[i];
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  const float r = rsqrtf(ss / (float)HD + 1e-6f);
+#pragma unroll
+  for (int i = 0; i < 24; i++) v[i] *= r;
+}
+
+// Self attention of (sample b, head h) over its Tv action tokens. Wave w prepares tokens
+// 16w..16w+15 (lane: token 16w + l%16, dims 24 (l/16) ..+23) into the LDS Q/K/V^T fragments
+// (zeros past Tv), then attends with query tile w.
+constexpr uint32_t S_Q = 0, S_K = 12 * 1024, S_V = 24 * 1024;
+
+__device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, int l) {
+  const Layout& L = p.L;
+  const int w = wave_id(), lane = lane_id(), lr = lane & 15, g4 = lane >> 4;
+  const float* bq = p.b_qkv + (size_t)l * QKVN;
+#pragma unroll 1
+  for (int it = vwg(); it < p.B * NH; it += NWG) {
+    const int b = it / NH, h = it - b * NH;
+    const int tau = 16 * w + lr;
+    const bool tv = tau < p.Tv;
+    const int m = b * p.Tv + (tv ? tau : 0);
+    float qkv[3][24];
+    {
+      const int c0 = HD * h + 24 * g4;
+      const int cs[3] = {c0, D + c0, 2 * D + c0};
+      const float* const bs[3] = {bq + c0, bq + D + c0, bq + 2 * D + c0};
+      load24<3, 1>(ws, L.pqkv, L.ks_qkv, L.MP, QKVN, m, cs, bs, qkv);
+    }
+    float (&q)[24] = qkv[0];
+    float (&k)[24] = qkv[1];
+    float (&v)[24] = qkv[2];
+    rms96(q);
+    rms96(k);
+    // RoPE on split-half pairs (j, j + 48): lanes g4 = 0, 1 hold the low halves, g4 ^ 2 the partners
+    const bool lo = g4 < 2;
+    const int j0 = 24 * (g4 & 1);
+#pragma unroll
+    for (int i = 0; i < 24; i++) {
+      const float qo = __shfl_xor(q[i], 32, 64), ko = __shfl_xor(k[i], 32, 64);
+      const float c = p.rope_cos[(tv ? tau : 0) * 48 + j0 + i], sn = p.rope_sin[(tv ? tau : 0) * 48 + j0 + i];
+      q[i] = lo ? q[i] * c - qo * sn : qo * sn + q[i] * c;
+      k[i] = lo ? k[i] * c - ko * sn : ko * sn + k[i] * c;
+    }
+    __syncthreads();  // the previous item's readers are done with LDS
+    unsigned short* lq16 = reinterpret_cast<unsigned short*>(lds);
+#pragma unroll
+    for (int i = 0; i < 24; i++) {
+      const int d = 24 * g4 + i;
+      lq16[(S_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) >> 1] = tv ? bf16_bits(q[i]) : 0;
+      const uint32_t kr = kperm_row(tau);
+      lq16[(S_K + ((kr >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(kr, d)) >> 1] = tv ? bf16_bits(k[i]) : 0;
+      lq16[(S_V + ((d >> 4) * 2 + (tau >> 5)) * 1024 + frag_pos(d, tau)) >> 1] = tv ? bf16_bits(v[i]) : 0;
+    }
+    __syncthreads();
+    if (16 * w < p.Tv) {
+      u32x4 qf[3];
+#pragma unroll
+      for (int ks = 0; ks < 3; ks++) qf[ks] = lds128(S_Q + (w * 3 + ks) * 1024 + lane * 16);
+      unsigned vmask[2][4];
+#pragma unroll
+      for (int sp = 0; sp < 2; sp++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) vmask[sp][e] = 0xffffffffu;  // keys past Tv hold zeros
+      float mx, ps;
+      f32x4 o[6];
+      attend<4>(qf, S_K, S_V, p.Tv, vmask, mx, ps, o);
+      const int t = 16 * w + lr;
+      if (t < p.Tv) {
+        const int mo = b * p.Tv + t;
+#pragma unroll
+        for (int dt = 0; dt < 6; dt++)
+          st_b64(ws, (uint32_t)(L.attn + ((size_t)mo * D + HD * h + 16 * dt + 4 * g4) * 2),
+                 u32x2{pack_bf16x2(o[dt][0], o[dt][1]), pack_bf16x2(o[dt][2], o[dt][3])});
+      }
+    }
+  }
+}
+
+// Cross attention item (b, h, kc): context keys [128 kc, 128 kc + 128) of head h. The chunk's K
+// rows and V^T columns are copied to LDS (24 + 24 fragments); wave w prepares the query rows
+// 16w..16w+15 (sum of CQ partials + b_cq, per-head RMS) and attends with them.
+constexpr uint32_t C_Q = 0, C_K = 12 * 1024, C_V = 36 * 1024;
+
+__device__ __forceinline__ void stage_catt(const Params& p, rsrc_t ws, int l) {
+  const Layout& L = p.L;
+  const int w = wave_id(), lane = lane_id(), lr = lane & 15, g4 = lane >> 4;
+  const int nkc = (p.Lk + KCH - 1) / KCH;
+  const float* bq = p.b_cq + (size_t)l * D;
+#pragma unroll 1
+  for (int it = vwg(); it < p.B * NH * nkc; it += NWG) {
+    const int kc = it % nkc, rest = it / nkc, h = rest % NH, b = rest / NH;
+    const int key0 = kc * KCH, kvalid = min(KCH, p.Lk - key0);
+    const bf16* kb_ = p.kctx + ((size_t)b * p.NL + l) * p.Lkmax * D + HD * h;
+    const bf16* vb_ = p.vtctx + (((size_t)b * p.NL + l) * D + HD * h) * p.Lkmax;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // the previous item's readers are done with LDS
+#pragma unroll
+    for (int j = 0; j < 12; j++) {
+      const int f = w + 4 * j;  // 0..47
+      if (f < 24) {             // K fragment (key tile kt = f / 3, k-step f % 3)
+        const int kt = f / 3, ks = f - 3 * kt;
+        int key = key0 + 32 * (kt >> 1) + 8 * (lr >> 2) + 4 * (kt & 1) + (lr & 3);
+        if (key >= p.Lk) key = 0;
+        dma16<false>(kb_ + (size_t)key * D + ks * 32 + 8 * g4, lds_addr(C_K + f * 1024));
+      } else {  // V^T fragment (dim tile dt, span sp)
+        const int fv = f - 24, dt = fv >> 2, sp = fv & 3;
+        int kg = key0 + 32 * sp + 8 * g4;
+        if (kg >= p.Lk) kg = 0;
+        dma16<false>(vb_ + (size_t)(16 * dt + lr) * p.Lkmax + kg, lds_addr(C_V + fv * 1024));
+      }
+    }
+    // query rows of this wave
+    const int tau = 16 * w + lr;
+    const bool tv = tau < p.Tv;
+    float qq[1][24];
+    {
+      const int cs[1] = {HD * h + 24 * g4};
+      const float* const bs[1] = {bq + HD * h + 24 * g4};
+      load24<1, 4>(ws, L.pq, L.ks_d, L.MP, D, b * p.Tv + (tv ? tau : 0), cs, bs, qq);
+    }
+    float (&q)[24] = qq[0];
+    rms96(q);
+    unsigned short* lq16 = reinterpret_cast<unsigned short*>(lds);
+#pragma unroll
+    for (int i = 0; i < 24; i++) {
+      const int d = 24 * g4 + i;
+      lq16[(C_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) >> 1] = tv ? bf16_bits(q[i]) : 0;
+    }
+    unsigned vmask[4][4];
+#pragma unroll
+    for (int sp = 0; sp < 4; sp++) {
+      const int nv = min(max(kvalid - (32 * sp + 8 * g4), 0), 8);
+#pragma unroll
+      for (int e = 0; e < 4; e++) vmask[sp][e] = nv >= 2 * e + 2 ? 0xffffffffu : (nv == 2 * e + 1 ? 0xffffu : 0u);
+    }
+    vm_wait<0>();
+    __syncthreads();
+    if (16 * w < p.Tv) {
+      u32x4 qf[3];
+#pragma unroll
+      for (int ks = 0; ks < 3; ks++) qf[ks] = lds128(C_Q + (w * 3 + ks) * 1024 + lane * 16);
+      float mx, ps;
+      f32x4 o[6];
+      attend<8>(qf, C_K, C_V, kvalid, vmask, mx, ps, o);
+      const int t = 16 * w + lr;
+      if (t < p.Tv) {
+        const size_t prow = (((size_t)b * NH + h) * L.NKC + kc) * MAX_TV + t;
+#pragma unroll
+        for (int dt = 0; dt < 6; dt++)
+          st_b64(ws, (uint32_t)(L.cattp + (prow * HD + 16 * dt + 4 * g4) * 2),
+                 u32x2{pack_bf16x2(o[dt][0], o[dt][1]), pack_bf16x2(o[dt][2], o[dt][3])});
+        if (g4 == 0) st_b64(ws, (uint32_t)(L.cml + prow * 8), u32x2{as_u32(mx), as_u32(ps)});
+      }
+    }
+  }
+}
+
+// attn[b Tv + t][96 h + d] = sum_c w_c O_c; two rows per wave (32 lanes each, 24 lanes x 4 dims).
+__device__ __forceinline__ void stage_comb(const Params& p, rsrc_t ws) {
+  const Layout& L = p.L;
+  const int lane = lane_id(), half = lane >> 5, l32 = lane & 31;
+  const int nkc = (p.Lk + KCH - 1) / KCH;
+  const int rows = p.B * NH * p.Tv;
+#pragma unroll 1
+  for (int R0 = (vwg() * 4 + wave_id()) * 2; R0 < rows; R0 += NWG * 8) {
+    const int R = R0 + half;
+    const bool valid = R < rows && l32 < 24;
+    const int Rc = R < rows ? R : R0;
+    const int t = Rc % p.Tv, bh = Rc / p.Tv, h = bh % NH, b = bh / NH;
+    const size_t row0 = ((size_t)bh * L.NKC) * MAX_TV + t;
+    const int d0 = 4 * (l32 < 24 ? l32 : 0);
+    float Mx = -1e30f, den = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int c0 = 0; c0 < nkc; c0 += 8) {
+      u32x2 ml[8], v[8];
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        const size_t prow = row0 + (size_t)(c0 + c < nkc ? c0 + c : c0) * MAX_TV;
+        ml[c] = ldb64<kCpSc1>(ws, (uint32_t)(L.cml + prow * 8));
+        v[c] = ldb64<kCpSc1>(ws, (uint32_t)(L.cattp + (prow * HD + d0) * 2));
+      }
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        if (c0 + c >= nkc) break;
+        const float mc = as_f32(ml[c][0]), lc = as_f32(ml[c][1]);
+        const float mn = fmaxf(Mx, mc);
+        const float sa = exp2f(Mx - mn), sc = lc * exp2f(mc - mn);
+        Mx = mn;
+        den = den * sa + sc;
+        acc[0] = acc[0] * sa + sc * bf_lo(v[c][0]);
+        acc[1] = acc[1] * sa + sc * bf_hi(v[c][0]);
+        acc[2] = acc[2] * sa + sc * bf_lo(v[c][1]);
+        acc[3] = acc[3] * sa + sc * bf_hi(v[c][1]);
+      }
+    }
+    if (valid) {
+      const float inv = 1.0f / den;
+      st_b64(ws, (uint32_t)(L.attn + (((size_t)b * p.Tv + t) * D + HD * h + d0) * 2),
+             u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)});
+    }
+  }
+}
+
+// ---------------------------------------------------------------- the kernel
+constexpr uint32_t LDS_BYTES = 96 * 1024;
+
+__device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {
+  if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x == 0) {
+    const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+    p.stage_cycles[idx] += t1 - t0;
+    t0 = t1;
+  }
+}
+
+template <int WM, int WN>
+__global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
+  static_assert(GemmShape<WM, WN>::LDS <= LDS_BYTES, "LDS budget");
+  const Layout& L = p.L;
+  const rsrc_t ws = rsrc_all(p.ws);
+  const rsrc_t xtr = make_rsrc(p.x_t, (uint32_t)((size_t)p.B * p.xt_rows * AD * 4));
+  Grid grid;
+  grid.flags = reinterpret_cast<uint64_t*>(p.ws + OFF_FLAGS);
+  grid.err = reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 8);
+  const uint64_t seq = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
+  grid.e = seq << 32;
+  const int NL = p.NL;
+  const float dt = 1.0f / (float)p.S;
+  uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x < 16) p.stage_cycles[threadIdx.x] = 0;
+  GemmArgs gx{reinterpret_cast<const bf16*>(p.ws + L.xn), nullptr, D, D, L.M};
+  GemmArgs ga{reinterpret_cast<const bf16*>(p.ws + L.attn), nullptr, D, D, L.M};
+  GemmArgs gh{reinterpret_cast<const bf16*>(p.ws + L.h), nullptr, FF, FF, L.M};
+  auto sync = [&](int idx) {
+    mark(p, idx, t0);
+    grid_sync(grid);
+    mark(p, 15, t0);
+  };
+#pragma unroll 1
+  for (int step = 0; step < p.S; step++) {
+#pragma unroll 1
+    for (int l = 0; l < NL; l++) {
+      const float* mo = p.mods + ((size_t)step * NL + l) * 9 * D;  // [3 norms][scale, shift, gate][D]
+      if (l == 0) {
+        stage_norm<0>(p, ws, xtr, 0, nullptr, nullptr, mo, mo + D, 0.f);
+      } else {
+        const float* mp = mo - 9 * D;  // previous layer
+        stage_norm<1>(p, ws, xtr, L.ks_dn, p.b_dn + (size_t)(l - 1) * D, mp + 8 * D, mo, mo + D, 0.f);
+      }
+      sync(0);
+      {
+        EpiPartN e{{}, ws, (uint32_t)L.pqkv, L.MP, QKVN, 0};
+        gx.W = p.w_qkv + (size_t)l * QKVN * D;
+        gemm_stage<WM, WN>(gx, QKVN, D, L.ks_qkv, e);
+      }
+      sync(1);
+      stage_satt(p, ws, l);
+      sync(2);
+      {
+        EpiPartN e{{}, ws, (uint32_t)L.part, L.MP, D, 0};
+        ga.W = p.w_so + (size_t)l * D * D;
+        gemm_stage<WM, WN>(ga, D, D, L.ks_d, e);
+      }
+      sync(3);
+      stage_norm<1>(p, ws, xtr, L.ks_d, p.b_so + (size_t)l * D, mo + 2 * D, mo + 3 * D, mo + 4 * D, 0.f);
+      sync(4);
+      {
+        EpiPartN e{{}, ws, (uint32_t)L.pq, L.MP, D, 0};
+        gx.W = p.w_cq + (size_t)l * D * D;
+        gemm_stage<WM, WN>(gx, D, D, L.ks_d, e);
+      }
+      sync(5);
+      stage_catt(p, ws, l);
+      sync(6);
+      stage_comb(p, ws);
+      sync(7);
+      {
+        EpiPartN e{{}, ws, (uint32_t)L.part, L.MP, D, 0};
+        ga.W = p.w_co + (size_t)l * D * D;
+        gemm_stage<WM, WN>(ga, D, D, L.ks_d, e);
+      }
+      sync(8);
+      stage_norm<1>(p, ws, xtr, L.ks_d, p.b_co + (size_t)l * D, mo + 5 * D, mo + 6 * D, mo + 7 * D, 0.f);
+      sync(9);
+      {
+        EpiPartN e{{}, ws, (uint32_t)L.pgu, L.MP, GUN, 0};
+        gx.W = p.w_gu + (size_t)l * GUN * D;
+        gemm_stage<WM, WN>(gx, GUN, D, L.ks_gu, e);
+      }
+      sync(10);
+      stage_gate(p, ws, l);
+      sync(11);
+      {
+        EpiPartN e{{}, ws, (uint32_t)L.part, L.MP, D, 0};
+        gh.W = p.w_dn + (size_t)l * D * FF;
+        gemm_stage<WM, WN>(gh, D, FF, L.ks_dn, e);
+      }
+      sync(12);
+    }
+    const float* ml = p.mods + ((size_t)step * NL + NL - 1) * 9 * D;
+    const float* mf = p.mod_final + (size_t)step * 2 * D;
+    stage_norm<2>(p, ws, xtr, L.ks_dn, p.b_dn + (size_t)(NL - 1) * D, ml + 8 * D, mf, mf + D, dt);
+    sync(13);
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p.ws + OFF_CTRL), seq + 1, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Tile shapes: batches of up to 64 tokens use 32-token x 64-row tiles, larger ones 128 x 128.
+constexpr int SMALL_M = 64;
+__host__ inline bool small_cfg(int M) { return M <= SMALL_M; }
+
+}  // namespace ma2
+}  // namespace fa
+
+// ================================================================= host C ABI
+using namespace fa;
+
+extern "C" size_t fa_ma2_workspace_bytes(int batch, int Tv, int Lkmax) {
+  if (batch < 1 || Tv < 1 || Tv > ma2::MAX_TV || Lkmax < 16 || (size_t)batch * Tv > (size_t)ma2::MAX_TOKENS) return 0;
+  const bool sm = ma2::small_cfg(batch * Tv);
+  const size_t n = ma2::layout(batch, Tv, Lkmax, sm ? 32 : 128, sm ? 64 : 128).total;
+  return n < 0xffffffffull ? n : 0;
+}
+
+extern "C" int fa_ma2_max_batch(void) { return ma2::MAX_TOKENS / ma2::MAX_TV; }
+
+extern "C" int fa_ma2_workspace_init(void* workspace, size_t bytes, fa_stream_t stream) {
+  return fa_pi05_workspace_init(workspace, bytes, stream);
+}
+
+extern "C" int fa_ma2_read_status(const void* workspace, unsigned* status) {
+  return fa_pi05_read_status(workspace, status);
+}
+
+extern "C" int fa_ma2_flow(const fa_ma2_args* a, fa_stream_t stream) {
+  using namespace fa::ma2;
+  if (!a) return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: args is NULL");
+  if (a->weight_dtype != FA_DTYPE_BF16)
+    return host::fail(FA_ERR_UNSUPPORTED, "fa_ma2_flow: only bf16 weights are implemented (weight_dtype=%d)",
+                      a->weight_dtype);
+  const void* ptrs[] = {a->w_qkv, a->w_so, a->w_cq, a->w_co, a->w_gu, a->w_dn, a->b_qkv, a->b_so, a->b_cq,
+                        a->b_co, a->b_gu, a->b_dn, a->mods, a->mod_final, a->rope_cos, a->rope_sin, a->w_ain,
+                        a->b_ain, a->w_aout, a->b_aout, a->kctx, a->vtctx, a->x_t, a->workspace};
+  const char* names[] = {"w_qkv", "w_so", "w_cq", "w_co", "w_gu", "w_dn", "b_qkv", "b_so", "b_cq", "b_co",
+                         "b_gu", "b_dn", "mods", "mod_final", "rope_cos", "rope_sin", "w_ain", "b_ain",
+                         "w_aout", "b_aout", "kctx", "vtctx", "x_t", "workspace"};
+  for (int i = 0; i < 24; i++) {
+    if (!ptrs[i]) return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: %s is NULL", names[i]);
+    if (reinterpret_cast<uintptr_t>(ptrs[i]) & 15)
+      return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: %s is not 16-byte aligned", names[i]);
+  }
+  if (reinterpret_cast<uintptr_t>(a->workspace) & 255)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: workspace is not 256-byte aligned");
+  if (a->num_layers < 1 || a->num_steps < 1 || a->Tv < 1 || a->Tv > MAX_TV || a->Lk < 1 || a->adim < 0 ||
+      a->adim > AD || a->batch < 1)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: need num_layers>=1, num_steps>=1, 1<=Tv<=%d, Lk>=1, "
+                      "0<=adim<=32, batch>=1 (got NL=%d S=%d Tv=%d Lk=%d adim=%d batch=%d)", MAX_TV, a->num_layers,
+                      a->num_steps, a->Tv, a->Lk, a->adim, a->batch);
+  if (a->Lkmax < a->Lk || (a->Lkmax & 15))
+    return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: Lkmax=%d must be a multiple of 16 and >= Lk=%d", a->Lkmax,
+                      a->Lk);
+  if (a->xt_rows < a->Tv)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: xt_rows=%d < Tv=%d", a->xt_rows, a->Tv);
+  if ((size_t)a->batch * a->Tv > (size_t)MAX_TOKENS)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: batch x Tv = %d exceeds %d tokens", a->batch * a->Tv,
+                      MAX_TOKENS);
+  if ((size_t)a->batch * a->num_layers * a->Lkmax * D * 2 >= 0xffffffffull)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: context caches exceed the 4 GB buffer range");
+  const size_t need = fa_ma2_workspace_bytes(a->batch, a->Tv, a->Lkmax);
+  if (need == 0 || a->workspace_bytes < need)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: workspace_bytes=%zu < required %zu", a->workspace_bytes,
+                      need);
+  const bool sm = small_cfg(a->batch * a->Tv);
+  const void* kern = sm ? (const void*)ma2_kernel<1, 2> : (const void*)ma2_kernel<4, 4>;
+  int rc = host::check_device(kern, NTHR, LDS_BYTES, NWG, "fa_ma2_flow");
+  if (rc != FA_OK) return rc;
+  Params p;
+  p.w_qkv = static_cast<const bf16*>(a->w_qkv);
+  p.w_so = static_cast<const bf16*>(a->w_so);
+  p.w_cq = static_cast<const bf16*>(a->w_cq);
+  p.w_co = static_cast<const bf16*>(a->w_co);
+  p.w_gu = static_cast<const bf16*>(a->w_gu);
+  p.w_dn = static_cast<const bf16*>(a->w_dn);
+  p.b_qkv = a->b_qkv;
+  p.b_so = a->b_so;
+  p.b_cq = a->b_cq;
+  p.b_co = a->b_co;
+  p.b_gu = a->b_gu;
+  p.b_dn = a->b_dn;
+  p.mods = a->mods;
+  p.mod_final = a->mod_final;
+  p.rope_cos = a->rope_cos;
+  p.rope_sin = a->rope_sin;
+  p.w_ain = a->w_ain;
+  p.b_ain = a->b_ain;
+  p.w_aout = static_cast<const bf16*>(a->w_aout);
+  p.b_aout = a->b_aout;
+  p.kctx = static_cast<const bf16*>(a->kctx);
+  p.vtctx = static_cast<const bf16*>(a->vtctx);
+  p.x_t = a->x_t;
+  p.stage_cycles = a->stage_cycles;
+  p.ws = static_cast<unsigned char*>(a->workspace);
+  p.L = layout(a->batch, a->Tv, a->Lkmax, sm ? 32 : 128, sm ? 64 : 128);
+  p.NL = a->num_layers;
+  p.Lk = a->Lk;
+  p.Lkmax = a->Lkmax;
+  p.Tv = a->Tv;
+  p.adim = a->adim;
+  p.S = a->num_steps;
+  p.B = a->batch;
+  p.xt_rows = a->xt_rows;
+  void* args[] = {&p};
+  hipError_t e = hipLaunchCooperativeKernel(kern, dim3(NWG), dim3(NTHR), args, LDS_BYTES, (hipStream_t)stream);
+  if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_ma2_flow: cooperative launch failed: %s",
+                                         hipGetErrorString(e));
+  return FA_OK;
+}

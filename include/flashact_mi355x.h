@@ -118,7 +118,69 @@ size_t fa_pi05_workspace_bytes(int batch, int Tv, int Lmax);
 int fa_pi05_workspace_init(void* workspace, size_t bytes, fa_stream_t stream);
 /* Synchronous: copies the kernel status bits (FA_KSTATUS_*) of the last launch on this workspace. */
 int fa_pi05_read_status(const void* workspace, unsigned* status);
+/* Largest batch one launch accepts. batch 1 runs the latency-bound single-sample kernel, batch >= 2
+ * the batched (MFMA-bound) kernel; the workspace size depends on the batch (one workspace serves
+ * one batch size). */
 int fa_pi05_max_batch(void);
+
+/* ---------------------------------------------------------------- MolmoAct2 expert
+ * D=768, 8 heads of 96 (self attention over the action tokens, cross attention over the
+ * context), F=3072, action dim 32 of which the first `adim` are integrated; t_s = s/S, dt = +1/S.
+ * Weight packing is the reference's (benchmarks/molmoact2/eval_numerics.py:77-133), bf16:
+ *   w_qkv [NL][2304][768] (q | k | v rows), w_so / w_cq / w_co [NL][768][768],
+ *   w_gu [NL][6144][768] (rows 2f, 2f+1 = gate f, up f), w_dn [NL][768][3072]; w_aout [32][768].
+ * Biases fp32: b_qkv [NL][2304], b_so / b_cq / b_co / b_dn [NL][768], b_gu [NL][6144] (interleaved
+ * like w_gu), b_aout [32]; w_ain [768][32] and b_ain [768] fp32.
+ * mods [S][NL][3][3][768] ({self, cross, mlp} x {scale, shift, gate}), mod_final [S][2][768]
+ * (scale, shift). rope_cos/sin [Tv][48] for positions 0..Tv-1 (split-half pairs d, d+48).
+ * kctx bf16 [batch][NL][Lkmax][768] (rows [0, Lk) valid), vtctx bf16 [batch][NL][768][Lkmax]
+ * (columns [0, Lk) valid). x_t [batch][xt_rows][32] fp32 is updated in place for rows [0, Tv),
+ * dims [0, adim).
+ */
+typedef struct fa_ma2_args {
+  int weight_dtype; /* FA_DTYPE_BF16 */
+  const void* w_qkv;
+  const void* w_so;
+  const void* w_cq;
+  const void* w_co;
+  const void* w_gu;
+  const void* w_dn;
+  const float* b_qkv;
+  const float* b_so;
+  const float* b_cq;
+  const float* b_co;
+  const float* b_gu;
+  const float* b_dn;
+  const float* mods;
+  const float* mod_final;
+  const float* rope_cos;
+  const float* rope_sin;
+  const float* w_ain;
+  const float* b_ain;
+  const void* w_aout;
+  const float* b_aout;
+  const void* kctx;
+  const void* vtctx;
+  int Lk;
+  int Lkmax;
+  int Tv;
+  int adim;
+  int num_steps;
+  int num_layers; /* 36 for MolmoAct2 */
+  int batch;
+  float* x_t;
+  int xt_rows;
+  unsigned long long* stage_cycles; /* optional [16]: per-stage 100 MHz ticks, workgroup 0 */
+  void* workspace;
+  size_t workspace_bytes;
+} fa_ma2_args;
+
+/* Whole S-step flow loop for `batch` samples as ONE cooperative launch (256 workgroups). */
+int fa_ma2_flow(const fa_ma2_args* args, fa_stream_t stream);
+size_t fa_ma2_workspace_bytes(int batch, int Tv, int Lkmax);
+int fa_ma2_workspace_init(void* workspace, size_t bytes, fa_stream_t stream);
+int fa_ma2_read_status(const void* workspace, unsigned* status);
+int fa_ma2_max_batch(void);
 
 /* ---------------------------------------------------------------- common */
 int fa_device_query(int device, fa_device_info* info);

@@ -100,3 +100,45 @@ def test_batched_workspace_sizes(lib):
     assert 0 < b2 < b16 and b16 % 256 == 0 and one > 0
     assert lib.fa_pi05_workspace_bytes(16, 50, 2048) > b16
     assert lib.fa_pi05_workspace_bytes(lib.fa_pi05_max_batch() + 1, 50, 1024) == 0
+
+
+def _ma2_args(**kw):
+    a = _lib.Ma2Args()
+    fake = 1 << 20
+    for f in ("w_qkv", "w_so", "w_cq", "w_co", "w_gu", "w_dn", "b_qkv", "b_so", "b_cq", "b_co", "b_gu", "b_dn",
+              "mods", "mod_final", "rope_cos", "rope_sin", "w_ain", "b_ain", "w_aout", "b_aout", "kctx", "vtctx",
+              "x_t", "workspace"):
+        setattr(a, f, fake)
+    a.Lk, a.Lkmax, a.Tv, a.adim, a.num_steps, a.num_layers, a.batch, a.xt_rows = 493, 496, 30, 6, 10, 36, 1, 32
+    a.workspace_bytes = 1 << 30
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code,text", [
+    (dict(Tv=65, xt_rows=65), 1, "Tv"),
+    (dict(adim=33), 1, "adim"),
+    (dict(Lkmax=490), 1, "Lkmax"),
+    (dict(Lkmax=500), 1, "Lkmax"),
+    (dict(xt_rows=10), 1, "xt_rows"),
+    (dict(workspace_bytes=4096), 1, "workspace"),
+    (dict(w_gu=None), 1, "w_gu is NULL"),
+    (dict(vtctx=(1 << 20) + 4), 1, "vtctx is not 16-byte aligned"),
+    (dict(weight_dtype=1), 2, "bf16"),
+    (dict(batch=70), 1, "tokens"),
+])
+def test_ma2_rejects_bad_requests(lib, kw, code, text):
+    rc = lib.fa_ma2_flow(ctypes.byref(_ma2_args(**kw)), None)
+    assert rc == code
+    assert text in lib.fa_last_error().decode()
+
+
+def test_ma2_without_device(lib):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    assert lib.fa_ma2_flow(ctypes.byref(_ma2_args()), None) == 3
+    assert lib.fa_ma2_flow(ctypes.byref(_ma2_args(batch=16)), None) == 3
+    assert lib.fa_ma2_workspace_bytes(1, 30, 496) > 0
+    assert lib.fa_ma2_workspace_bytes(16, 30, 496) > lib.fa_ma2_workspace_bytes(1, 30, 496)

@@ -231,5 +231,80 @@ __device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int 
   }
 }
 
+// Split-K GEMM whose K-splits are summed inside the stage (for small tiles: one workgroup reads the
+// whole tile's partials, so large tiles leave the sum to the consumer stage instead): every split
+// stores its fp32 partial
+// [split][MP][N] (sc1), drains its stores, then bumps the tile's counter with a device-scope atomic.
+// The workgroup that brings the count to ksplit resets it, reads the ksplit partials of the tile in
+// split order (so the sum is deterministic) and hands fin(n, m, sum of columns n..n+3) for each of
+// the tile's rows m < M. Consumers then read one finished value instead of ksplit partials.
+// `counters` holds one zeroed word per output tile; `flag_lds` is an LDS word outside the GEMM ring.
+constexpr int FIXUP_MAX_KS = 16;
+
+template <int WM, int WN, class Fin>
+__device__ __forceinline__ void gemm_stage_fixup(const GemmArgs& g, int N, int K, int ksplit, rsrc_t ws,
+                                                 uint32_t part_off, int MP, unsigned* counters, uint32_t flag_lds,
+                                                 Fin& fin) {
+  using S = GemmShape<WM, WN>;
+  struct Part : NoPre {
+    rsrc_t ws;
+    uint32_t off;
+    int MP, N, split;
+    __device__ void operator()(int n0, int m, f32x4 v, Pre) const {
+      st_b128(ws, off + (uint32_t)((((size_t)split * MP + m) * N + n0) * 4), as_u32x4(v));
+    }
+  };
+  struct Direct : NoPre {  // ksplit == 1: the tile's own result is final
+    Fin* fin;
+    int split;
+    __device__ void operator()(int n0, int m, f32x4 v, Pre) const { (*fin)(n0, m, v); }
+  };
+  const int nm = (g.M + S::BM - 1) / S::BM, nn = N / S::BN;
+  const int items = nm * nn * ksplit, kc = K / ksplit;
+  if (ksplit == 1) {
+    Direct d{{}, &fin, 0};
+#pragma unroll 1
+    for (int it = vwg(); it < items; it += NWG) {
+      const int mt = it % nm, nt = it / nm;
+      gemm_tile<WM, WN>(g, mt * S::BM, nt * S::BN, 0, K, d);
+    }
+    return;
+  }
+  Part epi{{}, ws, part_off, MP, N, 0};
+  unsigned* flag = reinterpret_cast<unsigned*>(lds + flag_lds);
+  constexpr int Q = S::BN / 4;  // float4 columns per tile row
+#pragma unroll 1
+  for (int it = vwg(); it < items; it += NWG) {
+    const int mt = it % nm, rest = it / nm, nt = rest % nn, sp = rest / nn;
+    epi.split = sp;
+    gemm_tile<WM, WN>(g, mt * S::BM, nt * S::BN, sp * kc, sp * kc + kc, epi);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are complete
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned* c = counters + mt * nn + nt;
+      const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned last = old == (unsigned)ksplit - 1u;
+      if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) continue;
+#pragma unroll 1
+    for (int e = threadIdx.x; e < S::BM * Q; e += NTHR) {
+      const int m = mt * S::BM + e / Q, n = nt * S::BN + 4 * (e % Q);
+      if (m >= g.M) continue;
+      u32x4 v[FIXUP_MAX_KS];
+#pragma unroll
+      for (int s2 = 0; s2 < FIXUP_MAX_KS; s2++)
+        if (s2 < ksplit) v[s2] = ldb128<kCpSc1>(ws, part_off + (uint32_t)((((size_t)s2 * MP + m) * N + n) * 4));
+      f32x4 sum = as_f32x4(v[0]);
+#pragma unroll
+      for (int s2 = 1; s2 < FIXUP_MAX_KS; s2++)
+        if (s2 < ksplit) sum += as_f32x4(v[s2]);
+      fin(n, m, sum);
+    }
+  }
+}
+
 }  // namespace eng
 }  // namespace fa

@@ -4,21 +4,22 @@
 // dims integrated), t_s = s / S, dt = +1/S.
 //
 // Per layer (grid barrier after each stage), token m = b * Tv + t of sample b:
-//   N_msa  x = embed(x_t) (layer 0) or x += g_mlp * (sum of down partials + b_dn); h = adaRMS(x)
-//   QKV    [M x 2304] = h W_qkv^T, K split -> fp32 partials
-//   SATT   per (sample, head): sum partials + b_qkv, per-head RMS of q and k, RoPE (split-half
+//   N_msa  x = embed(x_t) (layer 0) or x += g_mlp * y (down projection); h = adaRMS(x)
+//   QKV    [M x 2304] = h W_qkv^T + b_qkv (K split: at small batch the last split of each tile
+//          sums the partials, at large batch the consumer stage does)
+//   SATT   per (sample, head): per-head RMS of q and k, RoPE (split-half
 //          pairs d, d+48 at position t), softmax(q k^T / sqrt(96)) v over the Tv action tokens
-//   SO     [M x 768] = attn W_so^T -> partials
-//   N_mca  x += g_msa * (sum + b_so); h = adaRMS(x)
-//   CQ     [M x 768] = h W_cq^T -> partials
-//   CATT   per (sample, head, 128-key chunk): q = RMS(sum + b_cq), attention over the context
+//   SO     [M x 768] = attn W_so^T + b_so
+//   N_mca  x += g_msa * y; h = adaRMS(x)
+//   CQ     [M x 768] = h W_cq^T + b_cq
+//   CATT   per (sample, head, 128-key chunk): q = RMS(q) per head, attention over the context
 //          keys (kctx rows, vtctx columns of head h) -> normalised partial O + (m, l)
 //   COMB   combine of the key chunks -> attn
-//   CO     [M x 768] = attn W_co^T -> partials
-//   N_mlp  x += g_mca * (sum + b_co); h = adaRMS(x)
-//   GU     [M x 6144] = h W_gu^T (rows 2f / 2f+1 = gate f / up f) -> partials
-//   GATE   m = silu(g + b_g) * (u + b_u) -> bf16
-//   DN     [M x 768] = m W_dn^T -> partials
+//   CO     [M x 768] = attn W_co^T + b_co
+//   N_mlp  x += g_mca * y; h = adaRMS(x)
+//   GU     [M x 6144] = h W_gu^T (rows 2f / 2f+1 = gate f / up f) -> m = silu(g + b_g) (u + b_u)
+//          (large batches: a GATE stage applies the activation to the summed partials)
+//   DN     [M x 768] = m W_dn^T + b_dn
 // then the final norm, action projection and Euler update of x_t[:, :adim].
 #include "engine.h"
 #include "../../include/flashact_mi355x.h"
@@ -32,12 +33,13 @@ constexpr int D = 768, NH = 8, HD = 96, FF = 3072, AD = 32, QKVN = 3 * D, GUN = 
 constexpr int KCH = 128;  // context keys per cross-attention item
 constexpr int MAX_TV = 64;
 constexpr int MAX_TOKENS = 2048;
-constexpr int MAX_KS = 16;
+constexpr int MAX_KS = FIXUP_MAX_KS;
 
 struct Layout {
   int B, Tv, M, MP, NKC;
   int ks_qkv, ks_d, ks_gu, ks_dn;  // K splits of QKV, the D x D projections, gate/up, down
-  size_t x, xn, attn, h, pqkv, pq, pgu, part, cattp, cml, total;
+  int ntiles;  // output tiles of the widest GEMM (one fixup counter each)
+  size_t x, xn, attn, h, pqkv, pq, pgu, part, yqkv, yq, yo, cnt, cattp, cml, total;
 };
 
 // K split for an [nm x N/BN] tile grid over K: the largest divisor of the 64-wide k-steps that
@@ -77,6 +79,11 @@ __host__ __device__ inline Layout layout(int B, int Tv, int Lkmax, int BM, int B
   L.pq = take((size_t)L.ks_d * L.MP * D * 4);
   L.pgu = take((size_t)L.ks_gu * L.MP * GUN * 4);
   L.part = take((size_t)ks_part * L.MP * D * 4);
+  L.yqkv = take((size_t)L.MP * QKVN * 4);
+  L.yq = take((size_t)L.MP * D * 4);
+  L.yo = take((size_t)L.MP * D * 4);
+  L.ntiles = nm * (GUN / BN);
+  L.cnt = take((size_t)L.ntiles * 4);
   L.cattp = take((size_t)B * NH * L.NKC * MAX_TV * HD * 2);
   L.cml = take((size_t)B * NH * L.NKC * MAX_TV * 8);
   L.total = o;
@@ -99,7 +106,28 @@ struct Params {
   int NL, Lk, Lkmax, Tv, adim, S, B, xt_rows;
 };
 
-struct EpiPartN : NoPre {  // fp32 partial sums [split][MP][N]
+struct FinBias {  // y[m][n..n+3] = sum + bias (fp32)
+  rsrc_t ws;
+  uint32_t off;
+  int N;
+  const float* bias;
+  __device__ void operator()(int n, int m, f32x4 v) const {
+    st_b128(ws, off + (uint32_t)(((size_t)m * N + n) * 4), as_u32x4(v + *reinterpret_cast<const f32x4*>(bias + n)));
+  }
+};
+
+struct FinSiluGate {  // columns 2f, 2f+1 = gate f, up f -> h[m][f] = silu(g + b_g) (u + b_u) (bf16)
+  rsrc_t ws;
+  uint32_t off;
+  const float* bias;
+  __device__ void operator()(int n, int m, f32x4 v) const {
+    const f32x4 b = *reinterpret_cast<const f32x4*>(bias + n);
+    st_b32(ws, off + (uint32_t)(((size_t)m * FF + (n >> 1)) * 2),
+           pack_bf16x2(silu(v[0] + b[0]) * (v[1] + b[1]), silu(v[2] + b[2]) * (v[3] + b[3])));
+  }
+};
+
+struct EpiPartN : NoPre {  // fp32 partial sums [split][MP][N] (summed by the consumer stage)
   rsrc_t ws;
   uint32_t off;
   int MP, N, split;
@@ -130,13 +158,22 @@ __device__ __forceinline__ void add_parts(rsrc_t ws, size_t base, int ks, int MP
   }
 }
 
+// The input y of a residual / attention stage: FIX = the finished projection (bias included, one
+// buffer), otherwise the sum of its `ks` K-split partials plus the bias.
+struct YSrc {
+  size_t fin;    // [MP][N] finished values (FIX)
+  size_t parts;  // [ks][MP][N] partials (otherwise)
+  int ks, N;
+  const float* bias;
+};
+
 // ---------------------------------------------------------------- norm rows
 // One wave per token row; lane holds columns 4 lane + 256 k + i (k < 3). MODE 0: x = embed(x_t);
-// MODE 1: x += gate * (sum of partials + bias); MODE 2: as 1, then the final norm, the action
-// projection and the Euler update of x_t[:, :adim].
-template <int MODE>
-__device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xtr, int ks, const float* bias,
-                                           const float* gate, const float* scale, const float* shift, float dt) {
+// MODE 1: x += gate * y (the previous projection, see YSrc); MODE 2: as 1, then the final norm,
+// the action projection and the Euler update of x_t[:, :adim].
+template <int MODE, bool FIX>
+__device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xtr, const YSrc& y, const float* gate,
+                                           const float* scale, const float* shift, float dt) {
   const Layout& L = p.L;
   const int lane = lane_id();
 #pragma unroll 1
@@ -168,16 +205,22 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
     } else {
       u32x4 xo[3];
       int cols[3];
-      f32x4 sum[3];
+      f32x4 yv[3];
 #pragma unroll
       for (int k = 0; k < 3; k++) {
         cols[k] = 4 * lane + 256 * k;
         xo[k] = ldb128<kCpSc1>(ws, (uint32_t)(L.x + ((size_t)m * D + cols[k]) * 4));
-        sum[k] = *reinterpret_cast<const f32x4*>(bias + cols[k]);
       }
-      add_parts<3, 4>(ws, L.part, ks, L.MP, D, m, cols, sum);
+      if (FIX) {
 #pragma unroll
-      for (int k = 0; k < 3; k++) x[k] = as_f32x4(xo[k]) + *reinterpret_cast<const f32x4*>(gate + cols[k]) * sum[k];
+        for (int k = 0; k < 3; k++) yv[k] = as_f32x4(ldb128<kCpSc1>(ws, (uint32_t)(y.fin + ((size_t)m * D + cols[k]) * 4)));
+      } else {
+#pragma unroll
+        for (int k = 0; k < 3; k++) yv[k] = *reinterpret_cast<const f32x4*>(y.bias + cols[k]);
+        add_parts<3, 4>(ws, y.parts, y.ks, L.MP, D, m, cols, yv);
+      }
+#pragma unroll
+      for (int k = 0; k < 3; k++) x[k] = as_f32x4(xo[k]) + *reinterpret_cast<const f32x4*>(gate + cols[k]) * yv[k];
     }
     float ss = 0.f;
 #pragma unroll
@@ -323,21 +366,28 @@ __device__ __forceinline__ void attend(const u32x4 (&qf)[3], uint32_t kbase, uin
   psum = ps;
 }
 
-// Sum + bias of 24 consecutive columns of each of the NT column bases c0[i] (row m of the
-// [ks][MP][N] partials): v[i][24].
-template <int NT, int PB>
-__device__ __forceinline__ void load24(rsrc_t ws, size_t base, int ks, int MP, int N, int m, const int (&c0)[NT],
-                                       const float* const (&bias)[NT], float (&v)[NT][24]) {
+// 24 consecutive columns c0[i].. of row m of the projection y (finished, or partials + bias), for
+// each of NT bases.
+template <int NT, bool FIX>
+__device__ __forceinline__ void load24(rsrc_t ws, const YSrc& y, int MP, int m, const int (&c0)[NT],
+                                       float (&v)[NT][24]) {
   int cols[6 * NT];
   f32x4 acc[6 * NT];
 #pragma unroll
   for (int t = 0; t < NT; t++)
 #pragma unroll
-    for (int q = 0; q < 6; q++) {
-      cols[6 * t + q] = c0[t] + 4 * q;
-      acc[6 * t + q] = *reinterpret_cast<const f32x4*>(bias[t] + 4 * q);
-    }
-  add_parts<6 * NT, PB>(ws, base, ks, MP, N, m, cols, acc);
+    for (int q = 0; q < 6; q++) cols[6 * t + q] = c0[t] + 4 * q;
+  if (FIX) {
+    u32x4 r[6 * NT];
+#pragma unroll
+    for (int i = 0; i < 6 * NT; i++) r[i] = ldb128<kCpSc1>(ws, (uint32_t)(y.fin + ((size_t)m * y.N + cols[i]) * 4));
+#pragma unroll
+    for (int i = 0; i < 6 * NT; i++) acc[i] = as_f32x4(r[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 6 * NT; i++) acc[i] = *reinterpret_cast<const f32x4*>(y.bias + cols[i]);
+    add_parts<6 * NT, (NT == 1 ? 4 : 1)>(ws, y.parts, y.ks, MP, y.N, m, cols, acc);
+  }
 #pragma unroll
   for (int t = 0; t < NT; t++)
 #pragma unroll
@@ -363,10 +413,10 @@ __device__ __forceinline__ void rms96(float (&v)[24]) {
 // (zeros past Tv), then attends with query tile w.
 constexpr uint32_t S_Q = 0, S_K = 12 * 1024, S_V = 24 * 1024;
 
-__device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, int l) {
+template <bool FIX>
+__device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, const YSrc& y) {
   const Layout& L = p.L;
   const int w = wave_id(), lane = lane_id(), lr = lane & 15, g4 = lane >> 4;
-  const float* bq = p.b_qkv + (size_t)l * QKVN;
 #pragma unroll 1
   for (int it = vwg(); it < p.B * NH; it += NWG) {
     const int b = it / NH, h = it - b * NH;
@@ -377,8 +427,7 @@ __device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, int l) {
     {
       const int c0 = HD * h + 24 * g4;
       const int cs[3] = {c0, D + c0, 2 * D + c0};
-      const float* const bs[3] = {bq + c0, bq + D + c0, bq + 2 * D + c0};
-      load24<3, 1>(ws, L.pqkv, L.ks_qkv, L.MP, QKVN, m, cs, bs, qkv);
+      load24<3, FIX>(ws, y, L.MP, m, cs, qkv);
     }
     float (&q)[24] = qkv[0];
     float (&k)[24] = qkv[1];
@@ -435,11 +484,11 @@ __device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, int l) {
 // 16w..16w+15 (sum of CQ partials + b_cq, per-head RMS) and attends with them.
 constexpr uint32_t C_Q = 0, C_K = 12 * 1024, C_V = 36 * 1024;
 
-__device__ __forceinline__ void stage_catt(const Params& p, rsrc_t ws, int l) {
+template <bool FIX>
+__device__ __forceinline__ void stage_catt(const Params& p, rsrc_t ws, int l, const YSrc& y) {
   const Layout& L = p.L;
   const int w = wave_id(), lane = lane_id(), lr = lane & 15, g4 = lane >> 4;
   const int nkc = (p.Lk + KCH - 1) / KCH;
-  const float* bq = p.b_cq + (size_t)l * D;
 #pragma unroll 1
   for (int it = vwg(); it < p.B * NH * nkc; it += NWG) {
     const int kc = it % nkc, rest = it / nkc, h = rest % NH, b = rest / NH;
@@ -469,8 +518,7 @@ __device__ __forceinline__ void stage_catt(const Params& p, rsrc_t ws, int l) {
     float qq[1][24];
     {
       const int cs[1] = {HD * h + 24 * g4};
-      const float* const bs[1] = {bq + HD * h + 24 * g4};
-      load24<1, 4>(ws, L.pq, L.ks_d, L.MP, D, b * p.Tv + (tv ? tau : 0), cs, bs, qq);
+      load24<1, FIX>(ws, y, L.MP, b * p.Tv + (tv ? tau : 0), cs, qq);
     }
     float (&q)[24] = qq[0];
     rms96(q);
@@ -557,7 +605,8 @@ __device__ __forceinline__ void stage_comb(const Params& p, rsrc_t ws) {
 }
 
 // ---------------------------------------------------------------- the kernel
-constexpr uint32_t LDS_BYTES = 96 * 1024;
+constexpr uint32_t RING_BYTES = 96 * 1024;       // GEMM ring / attention tiles
+constexpr uint32_t LDS_BYTES = RING_BYTES + 256;  // + the split-K fixup flag
 
 __device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {
   if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x == 0) {
@@ -569,7 +618,7 @@ __device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {
 
 template <int WM, int WN>
 __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
-  static_assert(GemmShape<WM, WN>::LDS <= LDS_BYTES, "LDS budget");
+  static_assert(GemmShape<WM, WN>::LDS <= RING_BYTES, "LDS budget");
   const Layout& L = p.L;
   const rsrc_t ws = rsrc_all(p.ws);
   const rsrc_t xtr = make_rsrc(p.x_t, (uint32_t)((size_t)p.B * p.xt_rows * AD * 4));
@@ -590,70 +639,73 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
     grid_sync(grid);
     mark(p, 15, t0);
   };
+  // Small tiles (FIX): the last K-split of each tile sums the partials and applies the bias (and
+  // the gate/up activation); large tiles: the consumer stage sums the partials (and a GATE stage
+  // applies the activation), which spreads the reduction over all workgroups.
+  constexpr bool FIX = WM == 1;
+  unsigned* cnt = reinterpret_cast<unsigned*>(p.ws + L.cnt);
+  auto gemm = [&](GemmArgs& g, const bf16* W, int N, int K, int ks, uint32_t part, uint32_t yfin, const float* bias) {
+    g.W = W;
+    if constexpr (FIX) {
+      FinBias f{ws, yfin, N, bias};
+      gemm_stage_fixup<WM, WN>(g, N, K, ks, ws, part, L.MP, cnt, RING_BYTES, f);
+    } else {
+      EpiPartN e{{}, ws, part, L.MP, N, 0};
+      gemm_stage<WM, WN>(g, N, K, ks, e);
+    }
+  };
 #pragma unroll 1
   for (int step = 0; step < p.S; step++) {
 #pragma unroll 1
     for (int l = 0; l < NL; l++) {
       const float* mo = p.mods + ((size_t)step * NL + l) * 9 * D;  // [3 norms][scale, shift, gate][D]
-      if (l == 0) {
-        stage_norm<0>(p, ws, xtr, 0, nullptr, nullptr, mo, mo + D, 0.f);
-      } else {
-        const float* mp = mo - 9 * D;  // previous layer
-        stage_norm<1>(p, ws, xtr, L.ks_dn, p.b_dn + (size_t)(l - 1) * D, mp + 8 * D, mo, mo + D, 0.f);
-      }
+      const YSrc ydn{L.yo, L.part, L.ks_dn, D, p.b_dn + (size_t)(l > 0 ? l - 1 : 0) * D};
+      const YSrc yso{L.yo, L.part, L.ks_d, D, p.b_so + (size_t)l * D};
+      const YSrc yco{L.yo, L.part, L.ks_d, D, p.b_co + (size_t)l * D};
+      const YSrc yqkv{L.yqkv, L.pqkv, L.ks_qkv, QKVN, p.b_qkv + (size_t)l * QKVN};
+      const YSrc ycq{L.yq, L.pq, L.ks_d, D, p.b_cq + (size_t)l * D};
+      if (l == 0)
+        stage_norm<0, FIX>(p, ws, xtr, ydn, nullptr, mo, mo + D, 0.f);
+      else
+        stage_norm<1, FIX>(p, ws, xtr, ydn, mo - 9 * D + 8 * D, mo, mo + D, 0.f);  // gate: mlp of layer l-1
       sync(0);
-      {
-        EpiPartN e{{}, ws, (uint32_t)L.pqkv, L.MP, QKVN, 0};
-        gx.W = p.w_qkv + (size_t)l * QKVN * D;
-        gemm_stage<WM, WN>(gx, QKVN, D, L.ks_qkv, e);
-      }
+      gemm(gx, p.w_qkv + (size_t)l * QKVN * D, QKVN, D, L.ks_qkv, (uint32_t)L.pqkv, (uint32_t)L.yqkv, yqkv.bias);
       sync(1);
-      stage_satt(p, ws, l);
+      stage_satt<FIX>(p, ws, yqkv);
       sync(2);
-      {
-        EpiPartN e{{}, ws, (uint32_t)L.part, L.MP, D, 0};
-        ga.W = p.w_so + (size_t)l * D * D;
-        gemm_stage<WM, WN>(ga, D, D, L.ks_d, e);
-      }
+      gemm(ga, p.w_so + (size_t)l * D * D, D, D, L.ks_d, (uint32_t)L.part, (uint32_t)L.yo, yso.bias);
       sync(3);
-      stage_norm<1>(p, ws, xtr, L.ks_d, p.b_so + (size_t)l * D, mo + 2 * D, mo + 3 * D, mo + 4 * D, 0.f);
+      stage_norm<1, FIX>(p, ws, xtr, yso, mo + 2 * D, mo + 3 * D, mo + 4 * D, 0.f);
       sync(4);
-      {
-        EpiPartN e{{}, ws, (uint32_t)L.pq, L.MP, D, 0};
-        gx.W = p.w_cq + (size_t)l * D * D;
-        gemm_stage<WM, WN>(gx, D, D, L.ks_d, e);
-      }
+      gemm(gx, p.w_cq + (size_t)l * D * D, D, D, L.ks_d, (uint32_t)L.pq, (uint32_t)L.yq, ycq.bias);
       sync(5);
-      stage_catt(p, ws, l);
+      stage_catt<FIX>(p, ws, l, ycq);
       sync(6);
       stage_comb(p, ws);
       sync(7);
-      {
-        EpiPartN e{{}, ws, (uint32_t)L.part, L.MP, D, 0};
-        ga.W = p.w_co + (size_t)l * D * D;
-        gemm_stage<WM, WN>(ga, D, D, L.ks_d, e);
-      }
+      gemm(ga, p.w_co + (size_t)l * D * D, D, D, L.ks_d, (uint32_t)L.part, (uint32_t)L.yo, yco.bias);
       sync(8);
-      stage_norm<1>(p, ws, xtr, L.ks_d, p.b_co + (size_t)l * D, mo + 5 * D, mo + 6 * D, mo + 7 * D, 0.f);
+      stage_norm<1, FIX>(p, ws, xtr, yco, mo + 5 * D, mo + 6 * D, mo + 7 * D, 0.f);
       sync(9);
-      {
+      gx.W = p.w_gu + (size_t)l * GUN * D;
+      if constexpr (FIX) {
+        FinSiluGate f{ws, (uint32_t)L.h, p.b_gu + (size_t)l * GUN};
+        gemm_stage_fixup<WM, WN>(gx, GUN, D, L.ks_gu, ws, (uint32_t)L.pgu, L.MP, cnt, RING_BYTES, f);
+      } else {
         EpiPartN e{{}, ws, (uint32_t)L.pgu, L.MP, GUN, 0};
-        gx.W = p.w_gu + (size_t)l * GUN * D;
         gemm_stage<WM, WN>(gx, GUN, D, L.ks_gu, e);
+        sync(10);
+        stage_gate(p, ws, l);
       }
-      sync(10);
-      stage_gate(p, ws, l);
       sync(11);
-      {
-        EpiPartN e{{}, ws, (uint32_t)L.part, L.MP, D, 0};
-        gh.W = p.w_dn + (size_t)l * D * FF;
-        gemm_stage<WM, WN>(gh, D, FF, L.ks_dn, e);
-      }
+      gemm(gh, p.w_dn + (size_t)l * D * FF, D, FF, L.ks_dn, (uint32_t)L.part, (uint32_t)L.yo,
+           p.b_dn + (size_t)l * D);
       sync(12);
     }
     const float* ml = p.mods + ((size_t)step * NL + NL - 1) * 9 * D;
     const float* mf = p.mod_final + (size_t)step * 2 * D;
-    stage_norm<2>(p, ws, xtr, L.ks_dn, p.b_dn + (size_t)(NL - 1) * D, ml + 8 * D, mf, mf + D, dt);
+    const YSrc ydn{L.yo, L.part, L.ks_dn, D, p.b_dn + (size_t)(NL - 1) * D};
+    stage_norm<2, FIX>(p, ws, xtr, ydn, ml + 8 * D, mf, mf + D, dt);
     sync(13);
   }
   if (blockIdx.x == 0 && threadIdx.x == 0)

@@ -8,7 +8,8 @@ Prints one JSON line: value = ms per chunk (lower is better), the roofline of th
 (algorithmic bytes / measured launch time vs 8 TB/s), the CPU fp32 oracle timed on the host
 cores (cpu_baseline), the parity of the first GPU chunk vs that oracle run, and "bs16": the
 metric's second half, chunks/s of the batch-16 launch and its MFMA
-utilisation (algorithmic FLOPs / launch time vs 2.5 PFLOP/s dense bf16).
+utilisation (algorithmic FLOPs / launch time vs 2.5 PFLOP/s dense bf16); "molmoact2": BASELINE
+config 4 at batch 1 (ms per chunk, HBM roofline fraction, parity vs the CPU oracle) and batch 16.
 """
 from __future__ import annotations
 
@@ -100,6 +101,96 @@ def bench_batched(dev, batch, steps, warmup, seed=0):
             "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "kernel_status": status}
 
 
+MA2 = dict(NL=36, D=768, H=8, HD=96, F=3072, AD=32, Lk=493, Tv=30, S=10, adim=6)
+
+
+def ma2_bytes_per_chunk(batch=1, c=MA2) -> int:
+    """HBM bytes of one MolmoAct2 launch: bf16 weights (once per step for the whole batch), every
+    sample's bf16 context K and V, fp32 biases and mods, action in/out projections; times S."""
+    D, F, NL = c["D"], c["F"], c["NL"]
+    params = 3 * D * D + 3 * D * D + 2 * F * D + D * F
+    weights = NL * params * 2
+    ctx = batch * NL * c["Lk"] * D * 2 * 2
+    biases = NL * (3 * D + 3 * D + 2 * F + D) * 4
+    mods = (NL * 9 * D + 2 * D) * 4
+    action_io = (D * c["AD"] + D) * 4 + c["AD"] * D * 2 + c["AD"] * 4
+    return c["S"] * (weights + ctx + biases + mods + action_io)
+
+
+def ma2_flops_per_launch(batch=1, c=MA2) -> int:
+    D, F, NL, Tv, Lk = c["D"], c["F"], c["NL"], c["Tv"], c["Lk"]
+    m = batch * Tv
+    proj = 2 * m * NL * (3 * D * D + 3 * D * D + 2 * F * D + D * F)
+    attn = batch * NL * c["H"] * Tv * (Tv + Lk) * c["HD"] * 2 * 2
+    action_io = 2 * m * c["AD"] * D * 2
+    return c["S"] * (proj + attn + action_io)
+
+
+def bench_ma2(dev, batch, launches, warmup=2, cpu=False, seed=0):
+    """MolmoAct2 expert, synthetic N(0, 0.02) weights and mods, N(0, 1) context."""
+    from flashact_amd import ma2
+    c = MA2
+    w = synthetic.ma2_weights(seed, dev, NL=c["NL"], S=c["S"])
+    inp = synthetic.ma2_inputs(seed + 1, dev, batch=batch, NL=c["NL"], Lk=c["Lk"], Tv=c["Tv"], adim=c["adim"])
+    ws, bs = ma2.pack_weights(w["w_qkv"], w["w_so"], w["w_cq"], w["w_co"], w["w_g"], w["w_u"], w["w_dn"],
+                              w["b_qkv"], w["b_so"], w["b_cq"], w["b_co"], w["b_g"], w["b_u"], w["b_dn"])
+    Lkmax = ma2.lkmax_for(c["Lk"])
+    kc, vt = ma2.make_context(inp["kctx"], inp["vctx"], Lkmax)
+    cos, sin = ma2.rope_table(c["Tv"], device=dev)
+    w_aout = w["w_aout"].to(torch.bfloat16)
+    x_t = inp["noise"].clone()
+
+    def launch():
+        ma2.launch(ws, bs, w["mods"], w["mod_final"], cos, sin, w["w_ain"], w["b_ain"], w_aout, w["b_aout"], kc, vt,
+                   c["Lk"], Lkmax, c["Tv"], c["adim"], c["S"], x_t)
+
+    launch()
+    torch.cuda.synchronize()
+    first = x_t.detach().cpu().numpy().copy()
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(launches):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / launches
+    nbytes = ma2_bytes_per_chunk(batch)
+    fl = ma2_flops_per_launch(batch)
+    out = {"workload": f"molmoact2_expert_bs{batch}_Tv30_Lk493_S10", "batch": batch, "ms_per_launch": round(ms, 3),
+           "chunks_per_s": round(batch / ms * 1e3, 1), "launches": launches,
+           "roofline": {"bound": "hbm", "algorithmic_bytes": nbytes,
+                        "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+           "achieved_tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+           "kernel_status": ma2.read_status(ma2.workspace(dev, batch, c["Tv"], Lkmax)),
+           "reference_published_ms": 30.75 if batch == 1 else None}
+    if cpu:
+        from oracle import oracle as O
+
+        def u16(t):
+            return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+        ow = {k: u16(w[k]) for k in ("w_qkv", "w_so", "w_cq", "w_co", "w_g", "w_u", "w_dn", "w_aout")}
+        ow.update({k: w[k].cpu().numpy() for k in ("b_qkv", "b_so", "b_cq", "b_co", "b_g", "b_u", "b_dn", "mods",
+                                                   "mod_final", "w_ain", "b_ain", "b_aout")})
+        ow.update(rope_cos=cos.cpu().numpy(), rope_sin=sin.cpu().numpy(), kctx=u16(inp["kctx"]),
+                  vctx=u16(inp["vctx"]))
+        t0 = time.perf_counter()
+        ref = O.ma2_flow(ow, inp["noise"].cpu().numpy(), Lk=c["Lk"], Tv=c["Tv"], S=c["S"], NL=c["NL"],
+                         adim=c["adim"])
+        cpu_ms = (time.perf_counter() - t0) * 1e3
+        a = first[..., :c["adim"]].astype(np.float64).ravel()
+        b = ref[..., :c["adim"]].astype(np.float64).ravel()
+        out["cpu_oracle_ms"] = round(cpu_ms, 1)
+        out["parity"] = {"max_abs": float(np.abs(a - b).max()), "mean_abs": float(np.abs(a - b).mean()),
+                         "cos": float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))}
+    return out
+
+
 def build_inputs(dev, seed=0):
     w = synthetic.pi05_weights(seed, dev, NL=NL)
     inp = synthetic.pi05_inputs(seed + 1, dev, batch=1, NL=NL, Lp=LP, Tv=TV)
@@ -142,6 +233,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline and parity check")
     ap.add_argument("--bs16-launches", type=int, default=10,
                     help="timed launches of the batch-16 kernel (BASELINE config 2); 0 skips it")
+    ap.add_argument("--ma2-launches", type=int, default=10,
+                    help="timed launches of the MolmoAct2 kernel at batch 1 and 16 (BASELINE config 4); 0 skips")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="first run a plain device copy of this many bytes (twice), the calibration dispatch for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
@@ -216,6 +309,9 @@ def main():
     }
     if args.bs16_launches > 0:
         res["bs16"] = bench_batched(dev, 16, args.bs16_launches, 2)
+    if args.ma2_launches > 0:
+        res["molmoact2"] = {"bs1": bench_ma2(dev, 1, args.ma2_launches, cpu=not args.no_cpu),
+                            "bs16": bench_ma2(dev, 16, args.ma2_launches)}
     if not args.no_cpu:
         cpu_ms, ref, threads = cpu_baseline(w, inp, mods, modf, cos, sin)
         d = np.abs(first[:TV].astype(np.float64) - ref[0].astype(np.float64))

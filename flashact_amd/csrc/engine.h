@@ -110,8 +110,14 @@ __device__ __forceinline__ void grid_sync(Grid& g) {
 // v_mfma_f32_16x16x32_bf16 (A operand = 16 weight rows, B operand = 16 tokens), so after the loop
 // lane l holds, for block (j, i), rows n = 16 (wn WN + j) + 4 (l / 16) + 0..3 of token
 // m = 16 (wm WM + i) + l % 16 -- four consecutive output features of one token.
-// Operands are staged per 64-k step in MFMA fragment order by global_load_lds (3-buffer ring, one
-// workgroup barrier per step). Rows m >= M copy row 0 (their results are discarded).
+//
+// Operands reach LDS by global_load_lds_dwordx4 in 128-wide k steps. A copy instruction that
+// touches 8 or 16 rows streams at ~38 GB/s per CU; one that touches 4 rows x 256 B streams at
+// ~145 GB/s (measured). So rows are taken in groups of 64: copy instruction r of a group loads
+// rows r, r+16, r+32, r+48 (k step = 256 B each, 16 lanes per row) and lands them as 4 x 256 B at
+// LDS pitch 1040 B. An MFMA fragment (16 rows of one 16-row block, 32 k) then reads row r from
+// copy r at 1040 r + 256 (block % 4) + 64 ks + 16 q: the 16 rows fall in 16 different bank groups.
+// Two-step ring, one workgroup barrier per step. Rows m >= M copy row 0 (results discarded).
 struct GemmArgs {
   const bf16* A;  // [M][lda] activations (written in this launch: sc1 copies)
   const bf16* W;  // [N][ldw] weights
@@ -121,10 +127,13 @@ struct GemmArgs {
 template <int WM, int WN>
 struct GemmShape {
   static constexpr int BM = 32 * WM, BN = 32 * WN;
-  static constexpr int NA = BM / 8, NW = BN / 8, NF = NA + NW;  // 1 KB fragments per 64-k step
-  static constexpr int FPW = NF / 4;                              // fragments per wave per step
-  static constexpr uint32_t STEP = NF * 1024;
-  static constexpr uint32_t LDS = 3 * STEP;
+  static constexpr int GA = (BM + 63) / 64, GW = (BN + 63) / 64;  // 64-row groups
+  static constexpr int NI = 16 * (GA + GW);                       // copy instructions per step
+  static constexpr int IPW = NI / 4;                              // per wave
+  static constexpr uint32_t PITCH = 1040;
+  static constexpr uint32_t STEP = (uint32_t)NI * PITCH;
+  static constexpr uint32_t LDS = 2 * STEP;
+  static_assert(BN % 64 == 0, "weight tiles are whole 64-row groups");
 };
 
 template <int WM, int WN, class Epi>
@@ -132,31 +141,31 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
   using S = GemmShape<WM, WN>;
   const int w = wave_id(), lane = lane_id(), lr = lane & 15, lq = lane >> 4;
   const int wm = w & 1, wn = w >> 1;
-  // this wave's fragments of every step: f = w + 4 j
-  const unsigned char* src[S::FPW];
+  // this wave's copy instructions of every step: f = w + 4 j; lane -> (row slot lq, 16-byte chunk lr)
+  const unsigned char* src[S::IPW];
 #pragma unroll
-  for (int j = 0; j < S::FPW; j++) {
+  for (int j = 0; j < S::IPW; j++) {
     const int f = w + 4 * j;
-    if (f < S::NA) {
-      int row = m0 + 16 * (f >> 1) + lr;
-      if (row >= g.M) row = 0;
-      src[j] = reinterpret_cast<const unsigned char*>(g.A + (size_t)row * g.lda + k0 + 32 * (f & 1) + 8 * lq);
+    if (f < 16 * S::GA) {
+      int row = m0 + 64 * (f >> 4) + 16 * lq + (f & 15);
+      if (row >= g.M || 64 * (f >> 4) + 16 * lq >= S::BM) row = 0;
+      src[j] = reinterpret_cast<const unsigned char*>(g.A + (size_t)row * g.lda + k0 + 8 * lr);
     } else {
-      const int fw = f - S::NA;
-      const int row = n0 + 16 * (fw >> 1) + lr;
-      src[j] = reinterpret_cast<const unsigned char*>(g.W + (size_t)row * g.ldw + k0 + 32 * (fw & 1) + 8 * lq);
+      const int fw = f - 16 * S::GA;
+      const int row = n0 + 64 * (fw >> 4) + 16 * lq + (fw & 15);
+      src[j] = reinterpret_cast<const unsigned char*>(g.W + (size_t)row * g.ldw + k0 + 8 * lr);
     }
   }
-  const int ns = (k1 - k0) >> 6;
+  const int ns = (k1 - k0) >> 7;
   auto issue = [&](int s) {
-    const uint32_t base = (uint32_t)(s % 3) * S::STEP;
+    const uint32_t base = (uint32_t)(s & 1) * S::STEP;
 #pragma unroll
-    for (int j = 0; j < S::FPW; j++) {
+    for (int j = 0; j < S::IPW; j++) {
       const int f = w + 4 * j;
-      if (f < S::NA)
-        dma16<true>(src[j] + 128 * s, lds_addr(base + f * 1024));
+      if (f < 16 * S::GA)
+        dma16<true>(src[j] + 256 * s, lds_addr(base + f * S::PITCH));
       else
-        dma16<false>(src[j] + 128 * s, lds_addr(base + f * 1024));
+        dma16<false>(src[j] + 256 * s, lds_addr(base + f * S::PITCH));
     }
   };
   f32x4 acc[WN][WM];
@@ -166,23 +175,25 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
     for (int i = 0; i < WM; i++) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   __builtin_amdgcn_s_waitcnt(0);  // earlier stores / loads of this wave are complete
   issue(0);
-  if (ns > 1) issue(1);
 #pragma unroll 1
   for (int s = 0; s < ns; s++) {
-    if (s + 1 < ns)
-      vm_wait<S::FPW>();
-    else
-      vm_wait<0>();
+    vm_wait<0>();
     __syncthreads();  // step s landed for every wave; every wave is done with step s - 1
-    if (s + 2 < ns) issue(s + 2);
-    const uint32_t base = (uint32_t)(s % 3) * S::STEP;
+    if (s + 1 < ns) issue(s + 1);
+    const uint32_t base = (uint32_t)(s & 1) * S::STEP;
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
+    for (int ks = 0; ks < 4; ks++) {
       u32x4 a[WM], b[WN];
 #pragma unroll
-      for (int i = 0; i < WM; i++) a[i] = lds128(base + ((wm * WM + i) * 2 + ks) * 1024 + lane * 16);
+      for (int i = 0; i < WM; i++) {
+        const int mb = wm * WM + i;  // 16-row block of A
+        a[i] = lds128(base + (16 * (mb >> 2) + lr) * S::PITCH + (mb & 3) * 256 + ks * 64 + lq * 16);
+      }
 #pragma unroll
-      for (int j = 0; j < WN; j++) b[j] = lds128(base + (S::NA + (wn * WN + j) * 2 + ks) * 1024 + lane * 16);
+      for (int j = 0; j < WN; j++) {
+        const int nb = wn * WN + j;
+        b[j] = lds128(base + (16 * (S::GA + (nb >> 2)) + lr) * S::PITCH + (nb & 3) * 256 + ks * 64 + lq * 16);
+      }
 #pragma unroll
       for (int j = 0; j < WN; j++)
 #pragma unroll
@@ -215,7 +226,7 @@ struct NoPre {
   __device__ Pre pre(int, int) const { return Pre{}; }
 };
 
-// Runs every tile of an [M x N] GEMM, K split into `ksplit` equal ranges (multiples of 64). Items
+// Runs every tile of an [M x N] GEMM, K split into `ksplit` equal ranges (multiples of 128). Items
 // are ordered m-tile fastest so the items of one weight tile run on neighbouring CUs of one XCD.
 // The epilogue receives the split index through epi.split.
 template <int WM, int WN, class Epi>

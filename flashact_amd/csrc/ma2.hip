@@ -42,10 +42,10 @@ struct Layout {
   size_t x, xn, attn, h, pqkv, pq, pgu, part, yqkv, yq, yo, cnt, cattp, cml, total;
 };
 
-// K split for an [nm x N/BN] tile grid over K: the largest divisor of the 64-wide k-steps that
+// K split for an [nm x N/BN] tile grid over K: the largest divisor of the 128-wide k steps that
 // keeps the item count within one pass of the 256 workgroups.
 __host__ __device__ inline int pick_ks(int nm, int nn, int K) {
-  const int steps = K / 64;
+  const int steps = K / 128;
   int best = 1;
   for (int ks = 1; ks <= steps && ks <= MAX_KS; ks++)
     if (steps % ks == 0 && nm * nn * ks <= NWG) best = ks;
@@ -605,7 +605,7 @@ __device__ __forceinline__ void stage_comb(const Params& p, rsrc_t ws) {
 }
 
 // ---------------------------------------------------------------- the kernel
-constexpr uint32_t RING_BYTES = 96 * 1024;       // GEMM ring / attention tiles
+constexpr uint32_t RING_BYTES = 136 * 1024;      // GEMM ring / attention tiles
 constexpr uint32_t LDS_BYTES = RING_BYTES + 256;  // + the split-K fixup flag
 
 __device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {

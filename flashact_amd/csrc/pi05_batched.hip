@@ -13,6 +13,7 @@
 //   O    [M x 1024] = attn Wo^T, K split 4 ways -> fp32 partials
 //   N2   x += gate_in * sum(partials); xn = adaRMS(x)
 //   GU   [M x 8192] = xn W2^T (gate/up rows interleaved) -> h = gelu_tanh(g) u [M x 4096]
+// (all GEMMs: 128-token x 128-row tiles, k steps of 128)
 //   DN   [M x 1024] = h W3^T, K split 4 ways -> fp32 partials
 // then the final norm, action projection and Euler update (src/pi05/mk6.cu:502-517).
 #include "engine.h"
@@ -469,8 +470,8 @@ __device__ __forceinline__ void stage_comb(const Params& p, rsrc_t ws) {
 }
 
 // ---------------------------------------------------------------- the kernel
-constexpr uint32_t LDS_BYTES = GemmShape<4, 8>::LDS;  // 144 KB: the largest stage footprint
-static_assert(GemmShape<4, 4>::LDS <= LDS_BYTES && ATT_LDS <= LDS_BYTES, "LDS budget");
+constexpr uint32_t LDS_BYTES = GemmShape<4, 4>::LDS > ATT_LDS ? GemmShape<4, 4>::LDS : ATT_LDS;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {
   if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x == 0) {
@@ -543,7 +544,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       {
         EpiGelu e{{}, ws, (uint32_t)L.h, 0};
         gx.W = p.w2 + (size_t)l * 8192 * D;
-        gemm_stage<4, 8>(gx, 8192, D, 1, e);
+        gemm_stage<4, 4>(gx, 8192, D, 1, e);
       }
       mark(p, 6, t0);
       grid_sync(grid);

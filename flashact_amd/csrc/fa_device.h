@@ -39,6 +39,24 @@ constexpr unsigned kErrSpin = 1u;   // a barrier wait hit its cap
 constexpr unsigned kErrXcd = 2u;    // blockIdx -> XCD mapping differs from the assumed round robin
 constexpr unsigned kSpinCap = 1u << 20;
 
+// Workspace rules shared by every kernel of the library, so that one workspace may serve any mix
+// of entry points and shapes:
+//  * Bytes [0, kWsDataBase) hold only control words (u64 launch sequence @0, u32 error bits @8,
+//    u32 exchange parity bases @12 and @16, u32 owner @kWsOwner), u64 epoch flags and the split-K
+//    fixup counters. Every kernel keeps its data at kWsDataBase and above.
+//  * Epoch flags derive from the launch sequence (epoch = seq << 32 + n), so a flag left by any
+//    earlier launch lies below every epoch of the current one.
+//  * Fixup counters are zero at rest (the last arriver resets its counter).
+//  * Parity-tagged exchange data is not self-invalidating: its parity sequence is only valid while
+//    the data area has been written by the same kernel since. The owner word names the kernel that
+//    last used the workspace; a parity-exchange kernel that finds another owner clears its exchange
+//    region and restarts its parity sequence before the first exchange.
+constexpr uint32_t kWsOwner = 20;
+constexpr uint32_t kWsCounters = 12288;  // [1024] u32
+constexpr uint32_t kWsMaxCounters = 1024;
+constexpr uint32_t kWsDataBase = 16384;
+constexpr unsigned kOwnerPi05Bs1 = 1, kOwnerPi05Batched = 2, kOwnerMa2Bs1 = 3, kOwnerMa2Generic = 4;
+
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
 }
@@ -137,6 +155,27 @@ __device__ __forceinline__ void poll_wave(const uint64_t* p, int n, uint64_t e, 
     }
     __builtin_amdgcn_s_sleep(1);
   }
+}
+
+// One full wave polls the u64 epoch flags at [off, off + bytes) of `ws` (bytes a multiple of
+// 1024) until every flag >= e; 16 bytes per lane and 1 KB per sc1 load round.
+__device__ __forceinline__ void poll_flags(rsrc_t ws, uint32_t off, uint32_t bytes, uint64_t e, unsigned* err) {
+  if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin) return;
+  const int lane = threadIdx.x & 63;
+  for (unsigned it = 0;; ++it) {
+    bool ok = true;
+    for (uint32_t o = 16u * lane; o < bytes; o += 1024u) {
+      const u32x4 v = ldb128<kCpSc1>(ws, off + o);
+      ok = ok && ((((uint64_t)v[1] << 32) | v[0]) >= e) && ((((uint64_t)v[3] << 32) | v[2]) >= e);
+    }
+    if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+    if (it > kSpinCap) {
+      if (lane == 0) atomicOr(err, kErrSpin);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");
 }
 
 // Publish this workgroup's epoch. All of the workgroup's prior global stores are complete

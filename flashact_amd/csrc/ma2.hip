@@ -22,12 +22,14 @@
 //   DN     [M x 768] = m W_dn^T + b_dn
 // then the final norm, action projection and Euler update of x_t[:, :adim].
 #include "engine.h"
+#include "ma2_attn.h"
 #include "../../include/flashact_mi355x.h"
 #include "fa_host.h"
 
 namespace fa {
 namespace ma2 {
 using namespace fa::eng;
+using namespace fa::ma2att;
 
 constexpr int D = 768, NH = 8, HD = 96, FF = 3072, AD = 32, QKVN = 3 * D, GUN = 2 * FF;
 constexpr int KCH = 128;  // context keys per cross-attention item
@@ -65,7 +67,7 @@ __host__ __device__ inline Layout layout(int B, int Tv, int Lkmax, int BM, int B
   L.ks_gu = pick_ks(nm, GUN / BN, D);
   L.ks_dn = pick_ks(nm, D / BN, FF);
   const int ks_part = L.ks_d > L.ks_dn ? L.ks_d : L.ks_dn;
-  size_t o = 4096;  // control block + 256 barrier slots
+  size_t o = kWsDataBase;  // control words, epoch flags and the fixup counters below
   auto take = [&](size_t n) {
     const size_t r = o;
     o += (n + 255) / 256 * 256;
@@ -83,7 +85,7 @@ __host__ __device__ inline Layout layout(int B, int Tv, int Lkmax, int BM, int B
   L.yq = take((size_t)L.MP * D * 4);
   L.yo = take((size_t)L.MP * D * 4);
   L.ntiles = nm * (GUN / BN);
-  L.cnt = take((size_t)L.ntiles * 4);
+  L.cnt = kWsCounters;  // fixed: never moves with the shape, so a reused workspace keeps them zero
   L.cattp = take((size_t)B * NH * L.NKC * MAX_TV * HD * 2);
   L.cml = take((size_t)B * NH * L.NKC * MAX_TV * 8);
   L.total = o;
@@ -293,79 +295,6 @@ __device__ __forceinline__ void stage_gate(const Params& p, rsrc_t ws, int l) {
 }
 
 // ---------------------------------------------------------------- attention pieces
-// LDS fragment layouts (1 KB per fragment, lane = row % 16 + 16 * ((k % 32) / 8), element k % 8):
-//   Q   (query tile qt, k-step ks)      rows = tokens
-//   K   (key tile kt, k-step ks)        row 4a + i of tile 2 sp + kt = key 32 sp + 8 a + 4 kt + i,
-//                                       so the S^T tiles (2 sp, 2 sp + 1) form the P^T operand of span sp
-//   V^T (dim tile dt, key span sp)      rows = dims, k = keys 32 sp .. 32 sp + 31 in order
-__device__ __forceinline__ uint32_t frag_pos(int row, int k) {
-  return (uint32_t)(((row & 15) + 16 * ((k & 31) >> 3)) * 16 + (k & 7) * 2);
-}
-__device__ __forceinline__ uint32_t kperm_row(int key) {  // key -> (tile * 16 + row) of the K layout
-  const int sp = key >> 5, o = key & 31;
-  return (uint32_t)((2 * sp + ((o & 7) >> 2)) * 16 + 4 * (o >> 3) + (o & 3));
-}
-
-// softmax(S^T) over NKT key tiles (keys 32 (kt/2) + 8 lq + 4 (kt%2) + i < kvalid), P^T operands,
-// then O^T = V^T P^T for the 6 dim tiles; returns (max, sum) and O^T (normalised by the sum).
-template <int NKT>
-__device__ __forceinline__ void attend(const u32x4 (&qf)[3], uint32_t kbase, uint32_t vbase, int kvalid,
-                                       const unsigned (&vmask)[NKT / 2][4], float& mx, float& psum, f32x4 (&o)[6]) {
-  const int lane = lane_id(), lq = lane >> 4;
-  const float qscale = 1.4426950408889634f * 0.10206207261596575f;  // log2(e) / sqrt(96)
-  f32x4 s[NKT];
-#pragma unroll
-  for (int kt = 0; kt < NKT; kt++) {
-    f32x4 a = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 3; ks++) a = mfma16(lds128(kbase + (kt * 3 + ks) * 1024 + lane * 16), qf[ks], a);
-    s[kt] = a;
-  }
-  float m_ = -1e30f;
-#pragma unroll
-  for (int kt = 0; kt < NKT; kt++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int key = 32 * (kt >> 1) + 8 * lq + 4 * (kt & 1) + i;
-      s[kt][i] = key < kvalid ? s[kt][i] * qscale : -1e30f;
-      m_ = fmaxf(m_, s[kt][i]);
-    }
-  m_ = fmaxf(m_, __shfl_xor(m_, 16, 64));
-  m_ = fmaxf(m_, __shfl_xor(m_, 32, 64));
-  float ps = 0.f;
-  u32x4 pb[NKT / 2];
-#pragma unroll
-  for (int sp = 0; sp < NKT / 2; sp++) {
-    float pv[8];
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        pv[4 * kt + i] = exp2f(s[2 * sp + kt][i] - m_);
-        ps += pv[4 * kt + i];
-      }
-    pb[sp] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
-                   pack_bf16x2(pv[6], pv[7])};
-  }
-  ps += __shfl_xor(ps, 16, 64);
-  ps += __shfl_xor(ps, 32, 64);
-  const float inv = 1.0f / ps;
-#pragma unroll
-  for (int dt = 0; dt < 6; dt++) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int sp = 0; sp < NKT / 2; sp++) {
-      u32x4 va = lds128(vbase + (dt * (NKT / 2) + sp) * 1024 + lane * 16);
-#pragma unroll
-      for (int e = 0; e < 4; e++) va[e] &= vmask[sp][e];
-      acc = mfma16(va, pb[sp], acc);
-    }
-    o[dt] = acc * inv;
-  }
-  mx = m_;
-  psum = ps;
-}
-
 // 24 consecutive columns c0[i].. of row m of the projection y (finished, or partials + bias), for
 // each of NT bases.
 template <int NT, bool FIX>
@@ -394,18 +323,6 @@ __device__ __forceinline__ void load24(rsrc_t ws, const YSrc& y, int MP, int m, 
     for (int q = 0; q < 6; q++)
 #pragma unroll
       for (int i = 0; i < 4; i++) v[t][4 * q + i] = acc[6 * t + q][i];
-}
-
-// RMS over the 96 dims of a head held by 4 lanes (xor 16, 32) as 24 values each.
-__device__ __forceinline__ void rms96(float (&v)[24]) {
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 24; i++) ss += v[i] * v[i];
-  ss += __shfl_xor(ss, 16, 64);
-  ss += __shfl_xor(ss, 32, 64);
-  const float r = rsqrtf(ss / (float)HD + 1e-6f);
-#pragma unroll
-  for (int i = 0; i < 24; i++) v[i] *= r;
 }
 
 // Self attention of (sample b, head h) over its Tv action tokens. Wave w prepares tokens
@@ -627,6 +544,9 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
   grid.err = reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 8);
   const uint64_t seq = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
   grid.e = seq << 32;
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(reinterpret_cast<unsigned*>(p.ws + kWsOwner), kOwnerMa2Generic, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   const int NL = p.NL;
   const float dt = 1.0f / (float)p.S;
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -725,6 +645,7 @@ using namespace fa;
 
 extern "C" size_t fa_ma2_workspace_bytes(int batch, int Tv, int Lkmax) {
   if (batch < 1 || Tv < 1 || Tv > ma2::MAX_TV || Lkmax < 16 || (size_t)batch * Tv > (size_t)ma2::MAX_TOKENS) return 0;
+  if (ma2_bs1_eligible(batch, Tv, Lkmax)) return ma2_bs1_workspace_bytes();
   const bool sm = ma2::small_cfg(batch * Tv);
   const size_t n = ma2::layout(batch, Tv, Lkmax, sm ? 32 : 128, sm ? 64 : 128).total;
   return n < 0xffffffffull ? n : 0;
@@ -778,6 +699,7 @@ extern "C" int fa_ma2_flow(const fa_ma2_args* a, fa_stream_t stream) {
   if (need == 0 || a->workspace_bytes < need)
     return host::fail(FA_ERR_INVALID_ARG, "fa_ma2_flow: workspace_bytes=%zu < required %zu", a->workspace_bytes,
                       need);
+  if (ma2_bs1_eligible(a->batch, a->Tv, a->Lkmax)) return ma2_bs1_launch(a, stream);
   const bool sm = small_cfg(a->batch * a->Tv);
   const void* kern = sm ? (const void*)ma2_kernel<1, 2> : (const void*)ma2_kernel<4, 4>;
   int rc = host::check_device(kern, NTHR, LDS_BYTES, NWG, "fa_ma2_flow");
@@ -809,6 +731,8 @@ extern "C" int fa_ma2_flow(const fa_ma2_args* a, fa_stream_t stream) {
   p.stage_cycles = a->stage_cycles;
   p.ws = static_cast<unsigned char*>(a->workspace);
   p.L = layout(a->batch, a->Tv, a->Lkmax, sm ? 32 : 128, sm ? 64 : 128);
+  if (sm && (uint32_t)p.L.ntiles > kWsMaxCounters)
+    return host::fail(FA_ERR_UNSUPPORTED, "fa_ma2_flow: %d fixup tiles exceed %u counters", p.L.ntiles, kWsMaxCounters);
   p.NL = a->num_layers;
   p.Lk = a->Lk;
   p.Lkmax = a->Lkmax;

@@ -43,7 +43,7 @@ __host__ __device__ inline Layout layout(int B, int Tv, int Lmax) {
   L.MP = (L.M + 127) / 128 * 128;
   L.NQT = (NH * Tv + 15) / 16;
   L.NKC = (Lmax + KCH - 1) / KCH;
-  size_t o = 4096;  // control block + 256 barrier slots
+  size_t o = kWsDataBase;  // control words, epoch flags and counters below
   auto take = [&](size_t n) {
     const size_t r = o;
     o += (n + 255) / 256 * 256;
@@ -492,6 +492,9 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
   grid.err = reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 8);
   const uint64_t seq = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
   grid.e = seq << 32;
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(reinterpret_cast<unsigned*>(p.ws + kWsOwner), kOwnerPi05Batched, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   const int NL = p.NL;
   const float dt = -1.0f / (float)p.S;
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();

@@ -55,7 +55,7 @@ constexpr uint32_t OFF_XFLAG = 1024; // [8 XCD][32 rank][4 wave] u64 epochs
 // GEMM operands (xn, q, attention output, MLP activation h) are stored in MFMA fragment order:
 // [XCD][token tile of 16][k-step of 32][token % 16][k % 32 / 8][8 bf16], so each 1 KB fragment a
 // wave loads as the B operand is contiguous (see frag_off).
-constexpr uint32_t OFF_XN = 16384;                                  // [8][4][32][16][4][8] bf16
+constexpr uint32_t OFF_XN = kWsDataBase;                                  // [8][4][32][16][4][8] bf16
 constexpr uint32_t OFF_Q = OFF_XN + NX * TP * D * 2;                // [8][4][8][16][4][8] bf16
 constexpr uint32_t OFF_ATTP = OFF_Q + NX * TP * HD * 2;             // [8][32][64][256] bf16
 constexpr uint32_t OFF_ATTML = OFF_ATTP + NX * NCH * TP * HD * 2;   // [8][32][64][2] f32
@@ -70,6 +70,7 @@ constexpr int NSB = 3;                                              // suffix bl
 constexpr uint32_t OFF_KFR = OFF_XP + 2 * NX * TP * D * 4;
 constexpr uint32_t OFF_VFR = OFF_KFR + NX * NSB * 16384;
 constexpr uint32_t WS_BYTES = OFF_VFR + NX * NSB * 16384;
+static_assert(OFF_XFLAG + NX * NR * NCW * 8 <= kWsCounters, "flags stay below the fixup counters");
 
 // LDS layout (bytes)
 constexpr uint32_t L_CTL = RING * PAGE;        // u32 ready[2], consumed[4], abort
@@ -886,9 +887,11 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
   if (tid < 16) ctl_st(tid, 0u);
   if (tid == 0 && xcc_id() != (unsigned)c.g) atomicOr(c.err, kErrXcd);
   const uint64_t seq = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
-  const unsigned xbase =
+  unsigned xbase =
       __hip_atomic_load(reinterpret_cast<const unsigned*>(p.ws + OFF_CTRL + 12), __ATOMIC_RELAXED,
                         __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned owner =
+      __hip_atomic_load(reinterpret_cast<const unsigned*>(p.ws + kWsOwner), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();  // the only workgroup barrier: LDS control words are initialised
   if (c.wave >= NCW) {
     loader_main(p, c, c.wave - NCW);
@@ -896,6 +899,21 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
   }
   c.e = seq << 32;
   c.tr = nullptr;
+  if (owner != kOwnerPi05Bs1) {
+    // Another kernel used the workspace since this one last did: its data may sit in the exchange
+    // buffers with any parity. The compute waves clear them (parity 0), restart the parity
+    // sequence and pass one grid barrier before the first exchange.
+    xbase = 0;
+    constexpr uint32_t n16 = 2u * NX * TP * D * 4 / 16;
+    for (uint32_t i = blockIdx.x * (NCW * 64) + tid; i < n16; i += NWG * NCW * 64)
+      stb128<kCpSc1>(c.ws, OFF_XP + 16 * i, u32x4{0u, 0u, 0u, 0u});
+    __builtin_amdgcn_s_waitcnt(0);
+    c.e += 1;
+    if (c.lane == 0)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(p.ws + OFF_XFLAG) + (c.g * NR + c.r) * NCW + c.wave, c.e,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    poll_flags(c.ws, OFF_XFLAG, NX * NR * NCW * 8, c.e, c.err);
+  }
   const int NL = p.NL;
   const bool nw = c.wave < 2 && c.r + 32 * c.wave < p.Tv;  // this wave owns a token in norm stages
   if (nw && c.lane < AD)
@@ -979,6 +997,8 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
   if (blockIdx.x == 0 && c.wave == 0 && c.lane == 0) {
     __hip_atomic_store(reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 12), (xbase + (unsigned)(p.S * NL)) & 1u,
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(reinterpret_cast<unsigned*>(p.ws + kWsOwner), kOwnerPi05Bs1, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(reinterpret_cast<uint64_t*>(p.ws + OFF_CTRL), seq + 1, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }

@@ -45,8 +45,9 @@ def gpu_tensors(c, device):
                 w_aout=w["w_aout"].to(device).to(torch.bfloat16), b_aout=d("b_aout"))
 
 
-def run_gpu(c, device, g=None, samples=None, xt_rows=None, stage_cycles=None):
-    """One launch over ``samples`` (default: all); returns x_t [len(samples)][Tv][32] numpy."""
+def run_gpu(c, device, g=None, samples=None, xt_rows=None, stage_cycles=None, ws=None):
+    """One launch over ``samples`` (default: all); returns x_t [len(samples)][Tv][32] numpy.
+    ``ws``: a caller-owned workspace tensor (default: the per-device cached one)."""
     g = g or gpu_tensors(c, device)
     samples = list(range(c["batch"])) if samples is None else list(samples)
     kc = g["kc"][samples].contiguous()
@@ -55,7 +56,8 @@ def run_gpu(c, device, g=None, samples=None, xt_rows=None, stage_cycles=None):
     x_t = torch.zeros(len(samples), rows, 32, dtype=torch.float32, device=device)
     x_t[:, :c["Tv"]] = c["inp"]["noise"][samples].to(device)
     ma2.launch(g["ws"], g["bs"], g["mods"], g["mod_final"], g["cos"], g["sin"], g["w_ain"], g["b_ain"], g["w_aout"],
-               g["b_aout"], kc, vt, c["Lk"], g["Lkmax"], c["Tv"], c["adim"], c["S"], x_t, stage_cycles=stage_cycles)
+               g["b_aout"], kc, vt, c["Lk"], g["Lkmax"], c["Tv"], c["adim"], c["S"], x_t, stage_cycles=stage_cycles,
+               workspace_tensor=ws)
     torch.cuda.synchronize(device)
     return x_t.cpu().numpy()
 

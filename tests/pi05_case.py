@@ -52,7 +52,7 @@ def gpu_tensors(c, device):
                 w_aout=w["w_aout"].to(device), b_aout=w["b_aout"].to(device))
 
 
-def run_gpu(c, device, g=None, stage_cycles=None, xt_rows=None, sample=0):
+def run_gpu(c, device, g=None, stage_cycles=None, xt_rows=None, sample=0, ws=None):
     """One launch for sample ``sample``; returns (x_t [Tv][32] numpy, kcache, vtcache)."""
     g = g or gpu_tensors(c, device)
     p = g["packed"]
@@ -63,7 +63,8 @@ def run_gpu(c, device, g=None, stage_cycles=None, xt_rows=None, sample=0):
     empty = torch.empty(0, device=device)
     pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], empty, empty, empty, empty, g["mods"], g["mod_final"],
                 g["cos"], g["sin"], g["w_ain"], g["b_ain"], g["w_aout"], g["b_aout"], None, None, 0,
-                kc, vc, c["Lp"], g["Lmax"], c["S"], c["Tv"], x_t, stage_cycles=stage_cycles)
+                kc, vc, c["Lp"], g["Lmax"], c["S"], c["Tv"], x_t, stage_cycles=stage_cycles,
+                workspace_tensor=ws)
     torch.cuda.synchronize(device)
     return x_t.cpu().numpy(), kc, vc
 
@@ -75,7 +76,7 @@ def parity(gpu_out: np.ndarray, ref: np.ndarray) -> dict:
     return {"max_abs": float(d.max()), "mean_abs": float(d.mean()), "cos": cos}
 
 
-def run_gpu_batched(c, device, g=None, xt_rows=None):
+def run_gpu_batched(c, device, g=None, xt_rows=None, ws=None):
     """One batched launch over all samples; returns (x_t [B][Tv][32] numpy, kcache, vtcache)."""
     g = g or gpu_tensors(c, device)
     p = g["packed"]
@@ -87,6 +88,6 @@ def run_gpu_batched(c, device, g=None, xt_rows=None):
     empty = torch.empty(0, device=device)
     pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], empty, empty, empty, empty, g["mods"], g["mod_final"],
                 g["cos"], g["sin"], g["w_ain"], g["b_ain"], g["w_aout"], g["b_aout"], None, None, 0,
-                kc, vc, c["Lp"], g["Lmax"], c["S"], c["Tv"], x_t)
+                kc, vc, c["Lp"], g["Lmax"], c["S"], c["Tv"], x_t, workspace_tensor=ws)
     torch.cuda.synchronize(device)
     return x_t.cpu().numpy(), kc, vc

@@ -61,6 +61,19 @@ class Ma2Args(ctypes.Structure):
     ]
 
 
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("weight_dtype", ctypes.c_int),
+        ("wqkv", ctypes.c_void_p), ("wo", ctypes.c_void_p), ("wgu", ctypes.c_void_p), ("wdn", ctypes.c_void_p),
+        ("ln_in", ctypes.c_void_p), ("ln_post", ctypes.c_void_p),
+        ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p),
+        ("x", ctypes.c_void_p), ("kcache", ctypes.c_void_p), ("vtcache", ctypes.c_void_p),
+        ("Lp", ctypes.c_int), ("Lmax", ctypes.c_int), ("num_layers", ctypes.c_int), ("batch", ctypes.c_int),
+        ("stage_cycles", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class DeviceInfo(ctypes.Structure):
     _fields_ = [("cus", ctypes.c_int), ("xcds", ctypes.c_int), ("lds_bytes", ctypes.c_int),
                 ("coop_launch", ctypes.c_int), ("coop_max_blocks", ctypes.c_int), ("arch", ctypes.c_char * 64)]
@@ -78,6 +91,8 @@ SYMBOLS = [
     ("fa_ma2_workspace_init", ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     ("fa_ma2_read_status", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint)]),
     ("fa_ma2_max_batch", ctypes.c_int, []),
+    ("fa_pi05_prefill", ctypes.c_int, [ctypes.POINTER(PrefillArgs), ctypes.c_void_p]),
+    ("fa_pi05_prefill_workspace_bytes", ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     ("fa_device_query", ctypes.c_int, [ctypes.c_int, ctypes.POINTER(DeviceInfo)]),
     ("fa_last_error", ctypes.c_char_p, []),
     ("fa_abi_version", ctypes.c_int, []),

@@ -55,7 +55,8 @@ constexpr uint32_t kWsOwner = 20;
 constexpr uint32_t kWsCounters = 12288;  // [1024] u32
 constexpr uint32_t kWsMaxCounters = 1024;
 constexpr uint32_t kWsDataBase = 16384;
-constexpr unsigned kOwnerPi05Bs1 = 1, kOwnerPi05Batched = 2, kOwnerMa2Bs1 = 3, kOwnerMa2Generic = 4;
+constexpr unsigned kOwnerPi05Bs1 = 1, kOwnerPi05Batched = 2, kOwnerMa2Bs1 = 3, kOwnerMa2Generic = 4,
+                   kOwnerPrefill = 5;
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);

@@ -14,6 +14,7 @@ import torch
 
 PI05 = dict(NL=18, D=1024, H=8, HD=256, F=4096, AD=32)
 PI05_BASELINE = dict(Lp=968, Tv=50, S=10)
+BACKBONE = dict(NL=18, D=2048, H=8, HD=256, F=16384)  # BASELINE config 3 (Gemma-2B shape)
 MA2 = dict(NL=36, D=768, H=8, HD=96, F=3072, AD=32)
 MA2_BASELINE = dict(Lk=493, Tv=30, S=10, adim=6)
 
@@ -55,6 +56,24 @@ def pi05_inputs(seed: int = 1, device="cpu", batch=1, NL=18, Lp=968, Tv=50, HD=2
     vpre = _normal(g, (batch, NL, Lp, HD), 1.0, device)
     noise = torch.randn(batch, Tv, AD, generator=g, device=device, dtype=torch.float32)
     return {"kpre": kpre, "vpre": vpre, "noise": noise}
+
+
+def backbone_weights(seed: int = 2, device="cpu", NL=18, D=2048, H=8, HD=256, F=16384, std=0.02):
+    """Natural-layout Gemma-2B-shaped backbone weights ([out][in], bf16) and the two RMSNorm weight
+    vectors per layer (bf16-valued float32)."""
+    g = _gen(seed, device)
+    n = lambda *s: _normal(g, s, std, device)  # noqa: E731
+    w = {"wq": n(NL, H * HD, D), "wk": n(NL, HD, D), "wv": n(NL, HD, D), "wo": n(NL, D, H * HD),
+         "wg": n(NL, F, D), "wu": n(NL, F, D), "wd": n(NL, D, F)}
+    w["ln_in"] = n(NL, D).float()
+    w["ln_post"] = n(NL, D).float()
+    return w
+
+
+def prefix_inputs(seed: int = 3, device="cpu", batch=1, Lp=968, D=2048):
+    """Prefix hidden states entering backbone layer 0: [batch][Lp][D] fp32 ~ N(0, 1)."""
+    g = _gen(seed, device)
+    return torch.randn(batch, Lp, D, generator=g, device=device, dtype=torch.float32)
 
 
 def ma2_weights(seed: int = 0, device="cpu", NL=36, D=768, F=3072, AD=32, S=10, std=0.02):

@@ -11,6 +11,9 @@
  *                            (kernel pi05_megakernel, src/pi05/mk6.cu:112-519)
  *   fa_ma2_flow ........... `launch(...)` of the mk_ma2 torch extension, src/molmoact2/binding.cpp:28-83
  *                            (kernel ma2_megakernel, src/molmoact2/mk_ma2.cu:103-576)
+ *   fa_pi05_prefill ....... the prefix prefill (openpi PaliGemma forward with use_cache,
+ *                            benchmarks/pi05/eval_numerics.py:50-57) and the K/V cache hand-off
+ *                            after it (src/pi05/pack_weights.py:60-70, eval_numerics.py:83-87)
  *   fa_*_workspace_bytes,
  *   fa_*_workspace_init ... the reference's caller-allocated scratch tensors
  *                            (src/pi05/binding.cpp:34-36, src/molmoact2/binding.cpp:33-34)
@@ -181,6 +184,50 @@ size_t fa_ma2_workspace_bytes(int batch, int Tv, int Lkmax);
 int fa_ma2_workspace_init(void* workspace, size_t bytes, fa_stream_t stream);
 int fa_ma2_read_status(const void* workspace, unsigned* status);
 int fa_ma2_max_batch(void);
+
+/* ---------------------------------------------------------------- pi0.5 prefix prefill
+ * The Gemma-2B-shaped backbone over the prefix: D=2048, 8 query heads / 1 KV
+ * head of 256, F=16384 GeLU-tanh-gated MLP, RMSNorm (eps 1e-6) scaled by (1 + w), RoPE (base
+ * 10000, split-half pairs j, j+128) at positions 0..Lp-1, bidirectional attention over the prefix.
+ * Replaces the reference's prefix prefill, openpi's PaliGemma forward with use_cache
+ * (benchmarks/pi05/eval_numerics.py:50-57), together with the cache hand-off after it (compact_kv,
+ * src/pi05/pack_weights.py:60-70, and the cache fill at benchmarks/pi05/eval_numerics.py:83-87):
+ * the launch writes the RoPE'd keys into kcache rows [0, Lp) and the transposed values into
+ * vtcache columns [0, Lp) of every layer, the layout fa_pi05_denoise reads.
+ * Weights bf16, packed like the expert's: wqkv [NL][2560][2048] (q/k RoPE pairs adjacent),
+ * wo [NL][2048][2048], wgu [NL][32768][2048] (rows 2f, 2f+1 = gate f, up f), wdn [NL][2048][16384].
+ * ln_in, ln_post [NL][2048] fp32: the input and post-attention RMSNorm weights of each layer.
+ * rope_cos/sin [Lp][128]. x [batch][Lp][2048] fp32: the hidden states entering layer 0 (the
+ * prefix embeddings after any embedding scaling). kcache [batch][NL][Lmax][256] and vtcache
+ * [batch][NL][256][Lmax] bf16, Lmax >= Lp. Of the last layer only the K/V projections run: its
+ * attention and MLP outputs reach no cache entry.
+ * The workspace is zeroed with fa_pi05_workspace_init and read with fa_pi05_read_status.
+ */
+typedef struct fa_prefill_args {
+  int weight_dtype; /* FA_DTYPE_BF16 */
+  const void* wqkv;
+  const void* wo;
+  const void* wgu;
+  const void* wdn;
+  const float* ln_in;
+  const float* ln_post;
+  const float* rope_cos;
+  const float* rope_sin;
+  const float* x;
+  void* kcache;
+  void* vtcache;
+  int Lp;
+  int Lmax;
+  int num_layers;
+  int batch;
+  unsigned long long* stage_cycles; /* optional [16]: per-stage 100 MHz ticks, workgroup 0 */
+  void* workspace;
+  size_t workspace_bytes;
+} fa_prefill_args;
+
+/* All layers of the prefix prefill as ONE cooperative launch (256 workgroups). */
+int fa_pi05_prefill(const fa_prefill_args* args, fa_stream_t stream);
+size_t fa_pi05_prefill_workspace_bytes(int batch, int Lp, int Lmax);
 
 /* ---------------------------------------------------------------- common */
 int fa_device_query(int device, fa_device_info* info);

@@ -21,6 +21,11 @@
  *       cross-attn over per-layer context KV .... src/molmoact2/mk_ma2.cu:397-529
  *       SiLU-gated MLP ........................... src/molmoact2/mk_ma2.cu:246-251, 542-552
  *       final layer + masked Euler (dt = +1/S) .. src/molmoact2/mk_ma2.cu:558-571
+ *   Gemma-2B backbone prefix prefill ............ openpi PaliGemma forward with use_cache, called at
+ *       (config 3)                                benchmarks/pi05/eval_numerics.py:50-57 (openpi is
+ *                                                 absent: restated from the Gemma decoder layer and
+ *                                                 pinned against transformers' GemmaDecoderLayer);
+ *       K/V kept per layer ...................... src/pi05/pack_weights.py:60-70 (compact_kv)
  *
  * Weights use the reference's natural (unpacked) layouts, [out][in] row-major, stored as
  * bf16 bit patterns (uint16). Every value is converted exactly to fp32 and all arithmetic
@@ -437,5 +442,105 @@ int fo_ma2_flow(const fo_ma2_dims* dm, const uint16_t* w_qkv, const float* b_qkv
   }
   free(x); free(h); free(qkv); free(q); free(k); free(v); free(att); free(o); free(gg); free(uu);
   free(Kc); free(Vc); free(wa); free(act);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Gemma backbone prefix prefill                   */
+/* ------------------------------------------------------------------ */
+typedef struct {
+  int NL, D, H, HD, F, Lp, batch;
+} fo_prefill_dims;
+
+/* The prefix prefill the reference runs through openpi's PaliGemma forward with use_cache
+ * (benchmarks/pi05/eval_numerics.py:50-57), restated from the Gemma decoder layer:
+ *   h = x rsqrt(mean(x^2) + 1e-6) (1 + w_in); q = h Wq^T, k = h Wk^T, v = h Wv^T
+ *   RoPE on q and k at positions 0..Lp-1 (pairs j, j + HD/2, base 10000)
+ *   attn = softmax(q k^T / sqrt(HD)) v, every prefix token against every prefix token (the
+ *          prefix attends to itself without a mask), H query heads sharing the K/V head
+ *   x += attn Wo^T; h = rms(x) (1 + w_post); x += (gelu_tanh(h Wg^T) (h Wu^T)) Wd^T
+ * Output: the RoPE'd K and the V of every layer, kout/vout [batch][NL][Lp][HD] fp32 (the rows
+ * compact_kv keeps, src/pi05/pack_weights.py:60-70). The last layer stops after its K/V.
+ * Weights: bf16 bits, natural layouts wq [NL][H*HD][D], wk/wv [NL][HD][D], wo [NL][D][H*HD],
+ * wg/wu [NL][F][D], wd [NL][D][F]; ln_in/ln_post [NL][D] fp32; rope_cos/sin [Lp][HD/2];
+ * x_in [batch][Lp][D] fp32, the hidden states entering layer 0. */
+int fo_gemma_prefill(const fo_prefill_dims* dm, const uint16_t* wq, const uint16_t* wk, const uint16_t* wv,
+                     const uint16_t* wo, const uint16_t* wg, const uint16_t* wu, const uint16_t* wd,
+                     const float* ln_in, const float* ln_post, const float* rope_cos, const float* rope_sin,
+                     const float* x_in, float* kout, float* vout) {
+  const int NL = dm->NL, D = dm->D, H = dm->H, HD = dm->HD, F = dm->F, Lp = dm->Lp, B = dm->batch;
+  if (NL < 1 || D < 1 || H < 1 || HD < 2 || (HD & 1) || F < 1 || Lp < 1 || B < 1) return -1;
+  const int QD = H * HD, half = HD / 2;
+  const float scale = 1.0f / sqrtf((float)HD);
+  float* x = (float*)malloc(sizeof(float) * (size_t)Lp * D);
+  float* h = (float*)malloc(sizeof(float) * (size_t)Lp * D);
+  float* q = (float*)malloc(sizeof(float) * (size_t)Lp * QD);
+  float* k = (float*)malloc(sizeof(float) * (size_t)Lp * HD);
+  float* v = (float*)malloc(sizeof(float) * (size_t)Lp * HD);
+  float* att = (float*)malloc(sizeof(float) * (size_t)Lp * QD);
+  float* o = (float*)malloc(sizeof(float) * (size_t)Lp * D);
+  float* g = (float*)malloc(sizeof(float) * (size_t)Lp * F);
+  float* u = (float*)malloc(sizeof(float) * (size_t)Lp * F);
+  float* zero = (float*)calloc((size_t)D, sizeof(float));
+  for (int b = 0; b < B; b++) {
+    memcpy(x, x_in + (size_t)b * Lp * D, sizeof(float) * (size_t)Lp * D);
+    for (int l = 0; l < NL; l++) {
+      ada_rms(x, Lp, D, ln_in + (size_t)l * D, zero, h);
+      linear_bf16(h, Lp, D, wq + (size_t)l * QD * D, NULL, QD, q);
+      linear_bf16(h, Lp, D, wk + (size_t)l * HD * D, NULL, HD, k);
+      linear_bf16(h, Lp, D, wv + (size_t)l * HD * D, NULL, HD, v);
+      for (int t = 0; t < Lp; t++) {
+        const float* c = rope_cos + (size_t)t * half;
+        const float* sn = rope_sin + (size_t)t * half;
+        for (int hh = 0; hh <= H; hh++) {
+          float* vec = hh < H ? q + (size_t)t * QD + (size_t)hh * HD : k + (size_t)t * HD;
+          for (int j = 0; j < half; j++) {
+            float a0 = vec[j], a1 = vec[j + half];
+            vec[j] = a0 * c[j] - a1 * sn[j];
+            vec[j + half] = a1 * c[j] + a0 * sn[j];
+          }
+        }
+      }
+      float* ko = kout + ((size_t)b * NL + l) * Lp * HD;
+      float* vo = vout + ((size_t)b * NL + l) * Lp * HD;
+      memcpy(ko, k, sizeof(float) * (size_t)Lp * HD);
+      memcpy(vo, v, sizeof(float) * (size_t)Lp * HD);
+      if (l == NL - 1) break;
+#pragma omp parallel
+      {
+        float* p = (float*)malloc(sizeof(float) * (size_t)Lp);
+#pragma omp for schedule(static)
+        for (int th = 0; th < Lp * H; th++) {
+          int t = th / H, hh = th % H;
+          const float* qv = q + (size_t)t * QD + (size_t)hh * HD;
+          float mx = -INFINITY;
+          for (int j = 0; j < Lp; j++) {
+            p[j] = dot_f32(qv, k + (size_t)j * HD, HD) * scale;
+            if (p[j] > mx) mx = p[j];
+          }
+          float sum = 0.f;
+          for (int j = 0; j < Lp; j++) { p[j] = expf(p[j] - mx); sum += p[j]; }
+          float inv = 1.0f / sum;
+          float* out = att + (size_t)t * QD + (size_t)hh * HD;
+          for (int d = 0; d < HD; d++) out[d] = 0.f;
+          for (int j = 0; j < Lp; j++) {
+            float w = p[j] * inv;
+            const float* vr = v + (size_t)j * HD;
+            for (int d = 0; d < HD; d++) out[d] += w * vr[d];
+          }
+        }
+        free(p);
+      }
+      linear_bf16(att, Lp, QD, wo + (size_t)l * D * QD, NULL, D, o);
+      for (size_t i = 0; i < (size_t)Lp * D; i++) x[i] += o[i];
+      ada_rms(x, Lp, D, ln_post + (size_t)l * D, zero, h);
+      linear_bf16(h, Lp, D, wg + (size_t)l * F * D, NULL, F, g);
+      linear_bf16(h, Lp, D, wu + (size_t)l * F * D, NULL, F, u);
+      for (size_t i = 0; i < (size_t)Lp * F; i++) g[i] = gelu_tanh_f(g[i]) * u[i];
+      linear_bf16(g, Lp, F, wd + (size_t)l * D * F, NULL, D, o);
+      for (size_t i = 0; i < (size_t)Lp * D; i++) x[i] += o[i];
+    }
+  }
+  free(x); free(h); free(q); free(k); free(v); free(att); free(o); free(g); free(u); free(zero);
   return 0;
 }

@@ -31,6 +31,10 @@ class Pi05Dims(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("NL", "D", "H", "HD", "F", "AD", "Lp", "Tv", "S", "batch")]
 
 
+class PrefillDims(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("NL", "D", "H", "HD", "F", "Lp", "batch")]
+
+
 class Ma2Dims(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("NL", "D", "H", "HD", "F", "AD", "Lk", "Tv", "S", "adim", "batch")]
 
@@ -44,6 +48,7 @@ def lib():
         _lib.fo_num_threads.restype = ctypes.c_int
         _lib.fo_pi05_denoise.restype = ctypes.c_int
         _lib.fo_ma2_flow.restype = ctypes.c_int
+        _lib.fo_gemma_prefill.restype = ctypes.c_int
     return _lib
 
 
@@ -141,3 +146,28 @@ def ma2_flow(w: dict, x_t, *, Lk: int, Tv: int, S: int, NL: int, adim: int, D: i
     if rc != 0:
         raise ValueError(f"fo_ma2_flow rejected the dimensions (rc={rc})")
     return x
+
+
+def gemma_prefill(w: dict, x, *, NL: int, D: int = 2048, H: int = 8, HD: int = 256,
+                  F: int = 16384) -> tuple[np.ndarray, np.ndarray]:
+    """Prefix prefill through the Gemma backbone; returns (K, V), each [batch][NL][Lp][HD] fp32.
+
+    ``w`` keys: wq wk wv wo wg wu wd (uint16 bf16 bits, natural layouts), ln_in, ln_post, rope_cos,
+    rope_sin (fp32). ``x`` [batch][Lp][D] (or [Lp][D]) fp32: hidden states entering layer 0.
+    """
+    xx = _f32(x)
+    if xx.ndim == 2:
+        xx = xx[None]
+    B, Lp = xx.shape[0], xx.shape[1]
+    dims = PrefillDims(NL, D, H, HD, F, Lp, B)
+    u = {k: _u16(w[k]) for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")}
+    f = {k: _f32(w[k]) for k in ("ln_in", "ln_post", "rope_cos", "rope_sin")}
+    K = np.zeros((B, NL, Lp, HD), np.float32)
+    V = np.zeros((B, NL, Lp, HD), np.float32)
+    rc = lib().fo_gemma_prefill(ctypes.byref(dims), *[_p(u[k], np.uint16) for k in ("wq", "wk", "wv", "wo", "wg", "wu",
+                                                                                      "wd")],
+                                *[_p(f[k], np.float32) for k in ("ln_in", "ln_post", "rope_cos", "rope_sin")],
+                                _p(xx, np.float32), _p(K, np.float32), _p(V, np.float32))
+    if rc != 0:
+        raise ValueError(f"fo_gemma_prefill rejected the dimensions (rc={rc})")
+    return K, V

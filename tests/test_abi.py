@@ -142,3 +142,46 @@ def test_ma2_without_device(lib):
     assert lib.fa_ma2_flow(ctypes.byref(_ma2_args(batch=16)), None) == 3
     assert lib.fa_ma2_workspace_bytes(1, 30, 496) > 0
     assert lib.fa_ma2_workspace_bytes(16, 30, 496) > lib.fa_ma2_workspace_bytes(1, 30, 496)
+
+
+def _pf_args(**kw):
+    a = _lib.PrefillArgs()
+    fake = 1 << 20
+    for f in ("wqkv", "wo", "wgu", "wdn", "ln_in", "ln_post", "rope_cos", "rope_sin", "x", "kcache", "vtcache",
+              "workspace"):
+        setattr(a, f, fake)
+    a.Lp, a.Lmax, a.num_layers, a.batch = 968, 1024, 18, 1
+    a.workspace_bytes = 1 << 30
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code,text", [
+    (dict(Lp=0), 1, "Lp>=1"),
+    (dict(Lmax=960), 1, "Lmax"),
+    (dict(Lmax=1000), 1, "Lmax"),
+    (dict(batch=17), 1, "tokens"),
+    (dict(num_layers=0), 1, "num_layers"),
+    (dict(workspace_bytes=4096), 1, "workspace"),
+    (dict(wgu=None), 1, "wgu is NULL"),
+    (dict(x=(1 << 20) + 8), 1, "x is not 16-byte aligned"),
+    (dict(workspace=(1 << 20) + 16), 1, "workspace is not 256-byte aligned"),
+    (dict(weight_dtype=1), 2, "bf16"),
+])
+def test_prefill_rejects_bad_requests(lib, kw, code, text):
+    rc = lib.fa_pi05_prefill(ctypes.byref(_pf_args(**kw)), None)
+    assert rc == code
+    assert text in lib.fa_last_error().decode()
+
+
+def test_prefill_without_device(lib):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    assert lib.fa_pi05_prefill(ctypes.byref(_pf_args()), None) == 3
+    one = lib.fa_pi05_prefill_workspace_bytes(1, 968, 1024)
+    assert one > 0 and one % 256 == 0
+    assert lib.fa_pi05_prefill_workspace_bytes(4, 968, 1024) > one
+    assert lib.fa_pi05_prefill_workspace_bytes(1, 968, 960) == 0
+    assert lib.fa_pi05_prefill_workspace_bytes(17, 968, 1024) == 0

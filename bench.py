@@ -8,8 +8,10 @@ Prints one JSON line: value = ms per chunk (lower is better), the roofline of th
 (algorithmic bytes / measured launch time vs 8 TB/s), the CPU fp32 oracle timed on the host
 cores (cpu_baseline), the parity of the first GPU chunk vs that oracle run, and "bs16": the
 metric's second half, chunks/s of the batch-16 launch and its MFMA
-utilisation (algorithmic FLOPs / launch time vs 2.5 PFLOP/s dense bf16); "molmoact2": BASELINE
-config 4 at batch 1 (ms per chunk, HBM roofline fraction, parity vs the CPU oracle) and batch 16.
+utilisation (algorithmic FLOPs / launch time vs 2.5 PFLOP/s dense bf16); "config3": the
+Gemma-2B-shaped prefix prefill that writes the K/V cache (ms, MFMA utilisation) and the prefill +
+denoise chain; "molmoact2": BASELINE config 4 at batch 1 (ms per chunk, HBM
+roofline fraction, parity vs the CPU oracle) and batch 16.
 """
 from __future__ import annotations
 
@@ -35,6 +37,28 @@ MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 # WRITE_SIZE passes scaled by a 1 GiB device copy (profiles/pi05_denoise_bs1_traffic.md). Counters
 # cannot be read inside a timed run, so the figure is the last measured one for this kernel.
 TRAFFIC_BYTES = {"fetch": 15_709_937_267, "write": 2_475_342_645}
+
+
+# Stage counters (stage_cycles, workgroup 0, 100 MHz ticks) of each kernel: counter index -> stage.
+PI05_BS1_STAGES = {0: "N1", 1: "QKV", 2: "ATT", 3: "COMB", 4: "O", 5: "N2", 6: "GU", 7: "DN", 8: "FINAL",
+                   9: "XCD_waits"}
+PI05_BATCHED_STAGES = {0: "N1", 1: "QKV", 2: "ATT", 3: "COMB", 4: "O", 5: "N2", 6: "GU", 7: "DN", 8: "FINAL",
+                       9: "grid_barriers"}
+MA2_BS1_STAGES = {0: "N_msa", 1: "QKV", 2: "SATT", 3: "SO", 4: "N_mca", 5: "CQ", 6: "CATT", 7: "COMB", 8: "CO",
+                  9: "N_mlp", 10: "GU", 11: "DN", 12: "FINAL", 15: "XCD_waits"}
+MA2_STAGES = {0: "N_msa", 1: "QKV", 2: "SATT", 3: "SO", 4: "N_mca", 5: "CQ", 6: "CATT", 7: "COMB", 8: "CO",
+              9: "N_mlp", 10: "GU", 11: "GATE_or_GU", 12: "DN", 13: "FINAL", 15: "grid_barriers"}
+PREFILL_STAGES = {0: "N1", 1: "QKV", 2: "ATT", 3: "COMB", 4: "O", 5: "N2", 6: "GU", 7: "DN", 9: "grid_barriers"}
+
+
+def stage_us(dev, launch, names, per):
+    """One more launch with the per-stage tick counters of workgroup 0 -> microseconds per layer
+    (totals divided by `per`, the number of layer passes) for each stage."""
+    sc = torch.zeros(16, dtype=torch.int64, device=dev)
+    launch(sc)
+    torch.cuda.synchronize()
+    v = sc.cpu().numpy() / 100.0 / per
+    return {n: round(float(v[i]), 2) for i, n in names.items()}
 
 
 def algorithmic_bytes_per_chunk(nl=NL, lp=LP, tv=TV, s=S) -> int:
@@ -76,10 +100,10 @@ def bench_batched(dev, batch, steps, warmup, seed=0):
     x_t = inp["noise"].clone()
     empty = torch.empty(0, device=dev)
 
-    def launch():
+    def launch(sc=None):
         pi05.launch(packed["w1"], packed["wo"], packed["w2"], packed["w3"], empty, empty, empty, empty, mods, modf,
                     cos, sin, w["w_ain"], w["b_ain"], w["w_aout"], w["b_aout"], None, None, 0, kc, vc, LP, Lmax,
-                    S, TV, x_t)
+                    S, TV, x_t, stage_cycles=sc)
 
     for _ in range(warmup):
         launch()
@@ -98,7 +122,8 @@ def bench_batched(dev, batch, steps, warmup, seed=0):
     return {"workload": f"pi05_expert_bs{batch}_T50_Lp968_S10", "batch": batch, "chunks_per_s": round(batch / ms * 1e3, 1),
             "ms_per_launch": round(ms, 3), "launches": steps, "warmup": warmup, "flops_per_launch": fl,
             "achieved_tflops": round(tflops, 1), "mfma_peak_tflops": MFMA_PEAK_TFLOPS,
-            "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "kernel_status": status}
+            "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "kernel_status": status,
+            "stage_us_per_layer": stage_us(dev, launch, PI05_BATCHED_STAGES, NL * S)}
 
 
 MA2 = dict(NL=36, D=768, H=8, HD=96, F=3072, AD=32, Lk=493, Tv=30, S=10, adim=6)
@@ -140,9 +165,9 @@ def bench_ma2(dev, batch, launches, warmup=2, cpu=False, seed=0):
     w_aout = w["w_aout"].to(torch.bfloat16)
     x_t = inp["noise"].clone()
 
-    def launch():
+    def launch(sc=None):
         ma2.launch(ws, bs, w["mods"], w["mod_final"], cos, sin, w["w_ain"], w["b_ain"], w_aout, w["b_aout"], kc, vt,
-                   c["Lk"], Lkmax, c["Tv"], c["adim"], c["S"], x_t)
+                   c["Lk"], Lkmax, c["Tv"], c["adim"], c["S"], x_t, stage_cycles=sc)
 
     launch()
     torch.cuda.synchronize()
@@ -167,7 +192,9 @@ def bench_ma2(dev, batch, launches, warmup=2, cpu=False, seed=0):
                         "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
            "achieved_tflops": round(fl / (ms * 1e-3) / 1e12, 1),
            "kernel_status": ma2.read_status(ma2.workspace(dev, batch, c["Tv"], Lkmax)),
-           "reference_published_ms": 30.75 if batch == 1 else None}
+           "reference_published_ms": 30.75 if batch == 1 else None,
+           "stage_us_per_layer": stage_us(dev, launch, MA2_BS1_STAGES if batch == 1 else MA2_STAGES,
+                                          c["NL"] * c["S"])}
     if cpu:
         from oracle import oracle as O
 
@@ -189,6 +216,57 @@ def bench_ma2(dev, batch, launches, warmup=2, cpu=False, seed=0):
         out["parity"] = {"max_abs": float(np.abs(a - b).max()), "mean_abs": float(np.abs(a - b).mean()),
                          "cos": float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))}
     return out
+
+
+def prefill_flops(nl=NL, lp=LP) -> int:
+    """FLOPs of the Gemma-2B-shaped prefill as run: every layer's QKV, attention of the prefix over
+    itself (8 heads x 256, QK^T and PV), O, gate/up and down projections, except the last layer,
+    which stops after its K/V (its attention and MLP outputs reach no cache entry)."""
+    d, f, qkv = 2048, 16384, 2560
+    qkv_fl = 2 * lp * d * qkv
+    layer = qkv_fl + 2 * 2 * 8 * lp * lp * HD + 2 * lp * d * 2048 + 2 * lp * d * 2 * f + 2 * lp * f * d
+    return layer * (nl - 1) + qkv_fl
+
+
+def bench_prefill(dev, launches, step_fn, kc, vc, seed=5):
+    """Gemma-2B-shaped prefill of a 968-token N(0, 1) prefix (18 layers) writing the
+    expert's K/V cache, then the bs=1 denoise loop reading it. Times the prefill alone and the chain."""
+    from flashact_amd import prefill
+    w = synthetic.backbone_weights(seed, dev, NL=NL)
+    x = synthetic.prefix_inputs(seed + 1, dev, batch=1, Lp=LP)
+    packed = prefill.pack_backbone(w["wq"], w["wk"], w["wv"], w["wo"], w["wg"], w["wu"], w["wd"])
+    ln_in, ln_post = w["ln_in"].contiguous(), w["ln_post"].contiguous()
+    del w
+    cos, sin = prefill.rope_table(LP, device=dev)
+
+    def pf(sc=None):
+        prefill.prefill(packed, ln_in, ln_post, x, kc, vc, cos, sin, stage_cycles=sc)
+
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(2):
+        pf()
+        step_fn()
+    torch.cuda.synchronize()
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    e[0].record(stream)
+    for _ in range(launches):
+        pf()
+    e[1].record(stream)
+    for _ in range(launches):
+        pf()
+        step_fn()
+    e[2].record(stream)
+    torch.cuda.synchronize()
+    pf_ms = e[0].elapsed_time(e[1]) / launches
+    chain_ms = e[1].elapsed_time(e[2]) / launches
+    fl = prefill_flops()
+    status = prefill.read_status(prefill.workspace(dev, 1, LP, kc.shape[-2]))
+    return {"workload": "pi05_prefill_gemma2b_L18_Lp968 + pi05_expert_bs1_T50_S10", "launches": launches,
+            "prefill_ms": round(pf_ms, 3), "prefill_plus_denoise_ms": round(chain_ms, 3),
+            "prefill_flops": fl,
+            "mfma": {"achieved": round(fl / (pf_ms * 1e-3) / 1e12, 1), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(fl / (pf_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)},
+            "kernel_status": status, "stage_us_per_layer": stage_us(dev, pf, PREFILL_STAGES, NL - 1)}
 
 
 def build_inputs(dev, seed=0):
@@ -235,6 +313,8 @@ def main():
                     help="timed launches of the batch-16 kernel (BASELINE config 2); 0 skips it")
     ap.add_argument("--ma2-launches", type=int, default=10,
                     help="timed launches of the MolmoAct2 kernel at batch 1 and 16 (BASELINE config 4); 0 skips")
+    ap.add_argument("--prefill-launches", type=int, default=10,
+                    help="timed prefill launches and prefill + denoise chains (BASELINE config 3); 0 skips")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="first run a plain device copy of this many bytes (twice), the calibration dispatch for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
@@ -255,10 +335,10 @@ def main():
     x_t = inp["noise"][0].clone()
     empty = torch.empty(0, device=dev)
 
-    def step():
+    def step(sc=None):
         pi05.launch(packed["w1"], packed["wo"], packed["w2"], packed["w3"], empty, empty, empty, empty, mods, modf,
                     cos, sin, w["w_ain"], w["b_ain"], w["w_aout"], w["b_aout"], None, None, 0, kc, vc, LP, Lmax,
-                    S, TV, x_t)
+                    S, TV, x_t, stage_cycles=sc)
 
     step()  # first chunk: compared against the CPU oracle below
     torch.cuda.synchronize()
@@ -306,9 +386,21 @@ def main():
                      "kernel_ms_p50": round(float(np.median(per)), 4), "kernel_ms_min": round(float(per.min()), 4)},
         "wall_ms_per_step": round(t_wall * 1000.0 / args.steps, 4),
         "kernel_status": status,
+        "stage_us_per_layer": stage_us(dev, step, PI05_BS1_STAGES, NL * S),
     }
     if args.bs16_launches > 0:
         res["bs16"] = bench_batched(dev, 16, args.bs16_launches, 2)
+    if args.prefill_launches > 0:
+        kc3, vc3 = torch.zeros_like(kc), torch.zeros_like(vc)
+        x3 = inp["noise"][0].clone()
+
+        def step3():
+            pi05.launch(packed["w1"], packed["wo"], packed["w2"], packed["w3"], empty, empty, empty, empty, mods,
+                        modf, cos, sin, w["w_ain"], w["b_ain"], w["w_aout"], w["b_aout"], None, None, 0, kc3, vc3, LP,
+                        Lmax, S, TV, x3)
+
+        res["config3"] = bench_prefill(dev, args.prefill_launches, step3, kc3, vc3)
+        del kc3, vc3
     if args.ma2_launches > 0:
         res["molmoact2"] = {"bs1": bench_ma2(dev, 1, args.ma2_launches, cpu=not args.no_cpu),
                             "bs16": bench_ma2(dev, 16, args.ma2_launches)}

@@ -31,6 +31,10 @@ int check_device(const void* kernel, int threads, unsigned lds_bytes, int nwg, c
 size_t pi05_batched_workspace_bytes(int batch, int Tv, int Lmax);
 int pi05_denoise_batched(const fa_pi05_args* a, fa_stream_t stream);
 
+// K/V hand-off (srows > 0): enqueues the de-interleave / transpose of kvsrc_k / kvsrc_v into the
+// caches ahead of the denoise launch. Arguments are checked by fa_pi05_denoise.
+int pi05_kv_handoff(const fa_pi05_args* a, fa_stream_t stream);
+
 // Batch-1 MolmoAct2 launch (XCD-local layout), dispatched from fa_ma2_flow when eligible.
 bool ma2_bs1_eligible(int batch, int Tv, int Lkmax);
 size_t ma2_bs1_workspace_bytes();

@@ -371,6 +371,7 @@ int pi05_denoise_batched(const fa_pi05_args* a, fa_stream_t stream) {
   p.xt_rows = a->xt_rows;
   int rc = host::check_device((const void*)pb::pi05_batched_kernel, NTHR, LDS_BYTES, NWG, "fa_pi05_denoise");
   if (rc != FA_OK) return rc;
+  if (a->srows > 0 && (rc = pi05_kv_handoff(a, stream)) != FA_OK) return rc;
   void* args[] = {&p};
   hipError_t e = hipLaunchCooperativeKernel((const void*)pb::pi05_batched_kernel, dim3(NWG), dim3(NTHR), args, LDS_BYTES,
                                             (hipStream_t)stream);

@@ -1048,8 +1048,15 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
                       a->weight_dtype);
   if (a->s1 || a->so || a->s2 || a->s3)
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: fp8 row scales must be NULL for bf16 weights");
-  if (a->srows != 0 || a->kvsrc_k || a->kvsrc_v)
-    return host::fail(FA_ERR_UNSUPPORTED, "fa_pi05_denoise: the KV hand-off prologue (srows > 0) is not implemented");
+  if (a->srows < 0) return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: srows=%d < 0", a->srows);
+  if (a->srows > 0) {  // K/V hand-off from a prefill's cache rows (src/pi05/mk6.cu:258-277)
+    if (!a->kvsrc_k || !a->kvsrc_v)
+      return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: srows > 0 needs kvsrc_k and kvsrc_v");
+    if ((reinterpret_cast<uintptr_t>(a->kvsrc_k) | reinterpret_cast<uintptr_t>(a->kvsrc_v)) & 15)
+      return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: kvsrc_k / kvsrc_v are not 16-byte aligned");
+    if (a->srows < a->Lp)
+      return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: srows=%d < Lp=%d hand-off rows", a->srows, a->Lp);
+  }
   if (a->batch < 1 || a->batch > fa_pi05_max_batch())
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: batch=%d outside [1, %d]", a->batch, fa_pi05_max_batch());
   const void* ptrs[] = {a->w1, a->wo, a->w2, a->w3, a->mods, a->mod_final, a->rope_cos, a->rope_sin, a->w_ain,
@@ -1108,6 +1115,7 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
   p.S = a->num_steps;
   p.Tv = a->Tv;
   p.xt_rows = a->xt_rows;
+  if (a->srows > 0 && (rc = pi05_kv_handoff(a, stream)) != FA_OK) return rc;
   void* args[] = {&p};
   hipError_t e = hipLaunchCooperativeKernel((const void*)pi05_denoise_bs1, dim3(NWG), dim3(NTH), args, LDS_BYTES,
                                             (hipStream_t)stream);

@@ -90,7 +90,12 @@ typedef struct fa_pi05_args {
   const float* b_ain;
   const float* w_aout;
   const float* b_aout;
-  const void* kvsrc_k; /* KV hand-off source (srows > 0); reserved, must be NULL / 0 */
+  /* K/V hand-off (src/pi05/mk6.cu:258-277), used when srows > 0: kvsrc_k / kvsrc_v bf16
+   * [batch][NL][srows][256] hold a prefill's cache rows with RoPE on interleaved pairs (2d, 2d+1).
+   * Before the loop, rows [0, Lp) become kcache rows (pair -> dims d, d+128) and vtcache columns
+   * (transposed); srows >= Lp. This runs as a separate kernel ahead of the loop on the same stream.
+   * srows == 0: kcache / vtcache already hold the prefix and kvsrc_* are ignored. */
+  const void* kvsrc_k;
   const void* kvsrc_v;
   int srows;
   void* kcache;
@@ -122,8 +127,8 @@ int fa_pi05_workspace_init(void* workspace, size_t bytes, fa_stream_t stream);
 /* Synchronous: copies the kernel status bits (FA_KSTATUS_*) of the last launch on this workspace. */
 int fa_pi05_read_status(const void* workspace, unsigned* status);
 /* Largest batch one launch accepts. batch 1 runs the latency-bound single-sample kernel, batch >= 2
- * the batched (MFMA-bound) kernel; the workspace size depends on the batch (one workspace serves
- * one batch size). */
+ * the batched (MFMA-bound) kernel. The workspace size depends on the shape; one workspace that is
+ * large enough may serve any sequence of launches of every entry point (never two at once). */
 int fa_pi05_max_batch(void);
 
 /* ---------------------------------------------------------------- MolmoAct2 expert

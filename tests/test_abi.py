@@ -65,7 +65,10 @@ def _args(**kw):
     (dict(workspace_bytes=4096), 1, "workspace"),
     (dict(w2=None), 1, "w2 is NULL"),
     (dict(kcache=(1 << 20) + 8), 1, "kcache is not 16-byte aligned"),
-    (dict(srows=4), 2, "hand-off"),
+    (dict(srows=4), 1, "kvsrc_k"),
+    (dict(srows=900, kvsrc_k=1 << 20, kvsrc_v=1 << 20), 1, "srows=900 < Lp=968"),
+    (dict(srows=968, kvsrc_k=(1 << 20) + 2, kvsrc_v=1 << 20), 1, "not 16-byte aligned"),
+    (dict(srows=-1), 1, "srows"),
     (dict(weight_dtype=1), 2, "bf16"),
     (dict(batch=65), 1, "batch"),
     (dict(batch=0), 1, "batch"),

@@ -1,0 +1,176 @@
+"""pi0.5 policy wrapper: checkpoint loading and a ``predict`` call over the MI355X kernels.
+
+Mirrors the reference's ``HybridPi05`` (src/pi05/hybrid_model.py:23-228) minus its FlashRT
+front-end (vision encoder, tokenizer, encoder CUDA graph), which is outside this build:
+
+  * weights come from the same checkpoint keys (``paligemma_with_expert.gemma_expert.model.*``,
+    ``time_mlp_in/out``, ``action_in/out_proj``; hybrid_model.py:94-132), read from a
+    ``.safetensors`` file or a state dict; the backbone layers (for the prefill) from the PaliGemma
+    language-model keys of the same checkpoint;
+  * the adaRMS modulations are computed once on the device for the fixed schedule
+    t_i = 1 - i / num_steps (hybrid_model.py:111-128);
+  * ``predict`` takes the prefix either as hidden states (the backbone prefill runs on the GPU and
+    writes the expert's caches) or as the K/V rows of another prefill with interleaved RoPE pairs
+    (the reference's FlashRT hand-off, hybrid_model.py:199-221), draws the initial noise in the
+    reference's modes ("gaussian", "zero", "scale"; :206-211) and returns the raw chunk
+    [chunk_size][32] (the reference's ``return_raw``; un-normalisation needs FlashRT's norm stats).
+
+There is no fallback: every call runs the HIP kernels through the C ABI.
+"""
+from __future__ import annotations
+
+import os
+import re
+
+import numpy as np
+import torch
+
+from . import pi05, prefill
+
+EXPERT = "paligemma_with_expert.gemma_expert.model."
+D, HD, F, AD = 1024, 256, 4096, 32
+
+
+class _Source:
+    """Key -> tensor access over a state dict or a safetensors file (nothing is executed from it)."""
+
+    def __init__(self, source):
+        if isinstance(source, (str, os.PathLike)):
+            from safetensors import safe_open
+            self._h = safe_open(str(source), framework="pt", device="cpu")
+            self._keys = set(self._h.keys())
+            self._get = self._h.get_tensor
+        else:
+            self._keys = set(source.keys())
+            self._get = source.__getitem__
+
+    def keys(self):
+        return self._keys
+
+    def __getitem__(self, k):
+        return self._get(k)
+
+    def __contains__(self, k):
+        return k in self._keys
+
+
+def _count_layers(src, prefix):
+    pat = re.compile(re.escape(prefix) + r"layers\.(\d+)\.self_attn\.q_proj\.weight$")
+    ids = [int(m.group(1)) for k in src.keys() for m in [pat.match(k)] if m]
+    return max(ids) + 1 if ids else 0
+
+
+def find_backbone_prefix(src) -> str | None:
+    """The PaliGemma language-model layer prefix of an openpi checkpoint (it differs between
+    transformers versions): the prefix P with P + 'layers.0.self_attn.q_proj.weight' of width 2048."""
+    for k in sorted(src.keys()):
+        if k.endswith("layers.0.self_attn.q_proj.weight") and not k.startswith(EXPERT):
+            if src[k].shape[-1] == prefill.D:
+                return k[: -len("layers.0.self_attn.q_proj.weight")]
+    return None
+
+
+class Pi05Policy:
+    """Expert (and optionally backbone) weights resident on one GPU, ready for ``predict``."""
+
+    def __init__(self, checkpoint, *, num_steps: int = 10, chunk_size: int = 50, device="cuda",
+                 initial_noise_mode: str = "gaussian", initial_noise_scale: float = 1.0, load_backbone: bool = True):
+        if initial_noise_mode not in {"gaussian", "zero", "scale"}:
+            raise ValueError(f"unsupported initial noise mode: {initial_noise_mode}")
+        if not 1 <= chunk_size <= 64:
+            raise ValueError(f"chunk_size must be in [1, 64], got {chunk_size}")
+        self.num_steps, self.chunk_size = int(num_steps), int(chunk_size)
+        self.initial_noise_mode, self.initial_noise_scale = initial_noise_mode, float(initial_noise_scale)
+        self.device = torch.device(device)
+        src = _Source(checkpoint)
+        self.num_layers = _count_layers(src, EXPERT)
+        if self.num_layers == 0:
+            raise KeyError(f"no expert layers under {EXPERT!r} in the checkpoint")
+        self._load_expert(src)
+        self.backbone = None
+        if load_backbone:
+            bp = find_backbone_prefix(src)
+            if bp is not None:
+                self._load_backbone(src, bp)
+
+    # ------------------------------------------------------------------ loading
+    def _stack(self, src, prefix, name, n):
+        return torch.stack([src[f"{prefix}layers.{i}.{name}"].to(self.device) for i in range(n)])
+
+    def _load_expert(self, src):
+        NL, dev = self.num_layers, self.device
+        st = lambda n: self._stack(src, EXPERT, n, NL)  # noqa: E731
+        self.packed = pi05.pack_weights(st("self_attn.q_proj.weight"), st("self_attn.k_proj.weight"),
+                                        st("self_attn.v_proj.weight"), st("self_attn.o_proj.weight"),
+                                        st("mlp.gate_proj.weight"), st("mlp.up_proj.weight"),
+                                        st("mlp.down_proj.weight"))
+        f = lambda k: src[k].float().to(dev).contiguous()  # noqa: E731
+        self.mods, self.mod_final = pi05.precompute_mods(
+            self.num_steps, f("time_mlp_in.weight"), f("time_mlp_in.bias"), f("time_mlp_out.weight"),
+            f("time_mlp_out.bias"),
+            st("input_layernorm.dense.weight").float(), st("input_layernorm.dense.bias").float(),
+            st("post_attention_layernorm.dense.weight").float(), st("post_attention_layernorm.dense.bias").float(),
+            f(EXPERT + "norm.dense.weight"), f(EXPERT + "norm.dense.bias"))
+        self.w_ain, self.b_ain = f("action_in_proj.weight"), f("action_in_proj.bias")
+        self.w_aout, self.b_aout = f("action_out_proj.weight"), f("action_out_proj.bias")
+
+    def _load_backbone(self, src, bp):
+        n = _count_layers(src, bp)
+        if n != self.num_layers:
+            raise ValueError(f"backbone has {n} layers, the expert {self.num_layers}: each expert layer reads the "
+                             "same-index backbone layer's cache")
+        st = lambda name: self._stack(src, bp, name, n)  # noqa: E731
+        self.backbone = {
+            "packed": prefill.pack_backbone(st("self_attn.q_proj.weight"), st("self_attn.k_proj.weight"),
+                                            st("self_attn.v_proj.weight"), st("self_attn.o_proj.weight"),
+                                            st("mlp.gate_proj.weight"), st("mlp.up_proj.weight"),
+                                            st("mlp.down_proj.weight")),
+            "ln_in": st("input_layernorm.weight").float().contiguous(),
+            "ln_post": st("post_attention_layernorm.weight").float().contiguous(),
+        }
+
+    # ------------------------------------------------------------------ inference
+    def initial_noise(self, generator=None) -> torch.Tensor:
+        x = torch.zeros(self.chunk_size, AD, dtype=torch.float32, device=self.device)
+        if self.initial_noise_mode != "zero":
+            x.normal_(generator=generator)
+            if self.initial_noise_mode == "scale":
+                x.mul_(self.initial_noise_scale)
+        return x
+
+    def predict(self, prefix_hidden=None, *, kv_rows=None, noise=None, generator=None) -> np.ndarray:
+        """One action chunk [chunk_size][32] (raw, fp32).
+
+        prefix_hidden [Lp][2048] fp32: hidden states entering backbone layer 0 -> the prefill fills
+        the caches. Or kv_rows = (k_rows, v_rows) [NL][srows][256] bf16 with RoPE on interleaved
+        pairs plus the prefix length Lp as kv_rows[2] -> the hand-off fills them.
+        """
+        dev = self.device
+        if (prefix_hidden is None) == (kv_rows is None):
+            raise ValueError("pass exactly one of prefix_hidden and kv_rows")
+        if prefix_hidden is not None:
+            if self.backbone is None:
+                raise ValueError("the checkpoint has no backbone layers: pass kv_rows")
+            Lp = int(prefix_hidden.shape[-2])
+        else:
+            Lp = int(kv_rows[2])
+        Lmax = pi05.lmax_for(Lp, self.chunk_size)
+        kc = torch.zeros(self.num_layers, Lmax, HD, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros(self.num_layers, HD, Lmax, dtype=torch.bfloat16, device=dev)
+        ksrc = vsrc = None
+        srows = 0
+        if prefix_hidden is not None:
+            b = self.backbone
+            prefill.prefill(b["packed"], b["ln_in"], b["ln_post"], prefix_hidden.to(dev, torch.float32).contiguous(),
+                            kc, vc)
+        else:
+            ksrc, vsrc = kv_rows[0].contiguous(), kv_rows[1].contiguous()
+            srows = int(ksrc.shape[-2])
+        x_t = (noise.to(dev, torch.float32).clone() if noise is not None else self.initial_noise(generator))
+        cos, sin = pi05.rope_table(Lp, self.chunk_size, device=dev)
+        p = self.packed
+        empty = torch.empty(0, device=dev)
+        pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], empty, empty, empty, empty, self.mods, self.mod_final,
+                    cos, sin, self.w_ain, self.b_ain, self.w_aout, self.b_aout, ksrc, vsrc, srows, kc, vc, Lp, Lmax,
+                    self.num_steps, self.chunk_size, x_t)
+        return x_t.cpu().numpy()

@@ -313,6 +313,8 @@ def main():
                     help="timed launches of the batch-16 kernel (BASELINE config 2); 0 skips it")
     ap.add_argument("--ma2-launches", type=int, default=10,
                     help="timed launches of the MolmoAct2 kernel at batch 1 and 16 (BASELINE config 4); 0 skips")
+    ap.add_argument("--ref-shape-launches", type=int, default=20,
+                    help="timed bs=1 launches at the reference's published shape (Tv=10); 0 skips")
     ap.add_argument("--prefill-launches", type=int, default=10,
                     help="timed prefill launches and prefill + denoise chains (BASELINE config 3); 0 skips")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -390,6 +392,32 @@ def main():
     }
     if args.bs16_launches > 0:
         res["bs16"] = bench_batched(dev, 16, args.bs16_launches, 2)
+    if args.ref_shape_launches > 0:
+        # The reference's published loop number (9.5 ms, src/pi05/README.md:19) is for horizon 10
+        # (T = 16 padded) over a LIBERO prefix, fp8 weights, on an RTX 5090: the same kernel at Tv = 10.
+        tv10 = 10
+        cos10, sin10 = pi05.rope_table(LP, tv10, device=dev)
+        x10 = inp["noise"][0][:tv10].clone()
+
+        def step10():
+            pi05.launch(packed["w1"], packed["wo"], packed["w2"], packed["w3"], empty, empty, empty, empty, mods,
+                        modf, cos10, sin10, w["w_ain"], w["b_ain"], w["w_aout"], w["b_aout"], None, None, 0, kc, vc,
+                        LP, Lmax, S, tv10, x10)
+
+        for _ in range(3):
+            step10()
+        torch.cuda.synchronize()
+        e10 = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        e10[0].record(stream)
+        for _ in range(args.ref_shape_launches):
+            step10()
+        e10[1].record(stream)
+        torch.cuda.synchronize()
+        ms10 = e10[0].elapsed_time(e10[1]) / args.ref_shape_launches
+        res["reference_shape"] = {"workload": "pi05_expert_bs1_T10_Lp968_S10 (bf16)", "ms_per_chunk": round(ms10, 3),
+                                  "reference_published_ms": 9.5,
+                                  "reference_published_setup": "RTX 5090, fp8 weights, horizon 10 (T=16), LIBERO "
+                                                               "prefix, 10 steps (src/pi05/README.md:19)"}
     if args.prefill_launches > 0:
         kc3, vc3 = torch.zeros_like(kc), torch.zeros_like(vc)
         x3 = inp["noise"][0].clone()

@@ -32,7 +32,7 @@ MA2_SEQ = [  # (batch, Lk, Tv, S, adim); batch 1 with Tv <= 32 runs the batch-1 
     (1, 50, 31, 2, 32),   # all 32 dims integrated; at S = 1 (one Euler step of dt = 1) this
                           # case sits at the bf16-operand floor of ~2e-3 mean-abs
 ]
-PI05_SEQ = [(1, 200, 50, 2), (2, 200, 50, 2), (1, 150, 20, 1)]  # (batch, Lp, Tv, S)
+PI05_SEQ = [(1, 200, 50, 2), (2, 200, 50, 2), (1, 150, 20, 1), (1, 150, 64, 1)]  # (batch, Lp, Tv, S)
 
 
 def _shared_workspace(gpu):
@@ -86,3 +86,11 @@ def test_both_models_one_workspace(gpu):
     _pi05(gpu, ws, *PI05_SEQ[2], seed=26)
     _ma2(gpu, ws, *MA2_SEQ[4], seed=27)
     _ma2(gpu, ws, *MA2_SEQ[1], seed=28)
+
+
+def test_pi05_shape_sequence_one_workspace(gpu):
+    """pi0.5 on one workspace: a growing token count on the batch-1 kernel, the batched kernel in
+    between, then batch 1 again at the largest token count."""
+    ws = _shared_workspace(gpu)
+    for i, (B, Lp, Tv, S) in enumerate([(1, 200, 20, 2), (1, 200, 50, 2), (2, 150, 33, 1), (1, 150, 64, 1)]):
+        _pi05(gpu, ws, B, Lp, Tv, S, seed=41 + i)

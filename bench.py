@@ -218,6 +218,15 @@ def bench_ma2(dev, batch, launches, warmup=2, cpu=False, seed=0):
     return out
 
 
+def fp8_bytes_per_chunk(nl=NL, lp=LP, tv=TV, s=S) -> int:
+    """algorithmic_bytes_per_chunk with FP8-W8A16 weights: 1 byte per weight plus one fp32 scale per
+    packed row (2560 + 1024 + 8192 + 1024 rows per layer)."""
+    params_per_layer = (2560 * D) + (D * 2048) + (8192 * D) + (D * F)
+    bf16_weights = nl * params_per_layer * 2
+    fp8_weights = nl * params_per_layer + nl * (2560 + 1024 + 8192 + 1024) * 4
+    return algorithmic_bytes_per_chunk(nl, lp, tv, s) - s * (bf16_weights - fp8_weights)
+
+
 def prefill_flops(nl=NL, lp=LP) -> int:
     """FLOPs of the Gemma-2B-shaped prefill as run: every layer's QKV, attention of the prefix over
     itself (8 heads x 256, QK^T and PV), O, gate/up and down projections, except the last layer,
@@ -315,6 +324,8 @@ def main():
                     help="timed launches of the MolmoAct2 kernel at batch 1 and 16 (BASELINE config 4); 0 skips")
     ap.add_argument("--ref-shape-launches", type=int, default=20,
                     help="timed bs=1 launches at the reference's published shape (Tv=10); 0 skips")
+    ap.add_argument("--fp8-launches", type=int, default=20,
+                    help="timed bs=1 launches with FP8-W8A16 weights (Tv=50 and Tv=10); 0 skips")
     ap.add_argument("--prefill-launches", type=int, default=10,
                     help="timed prefill launches and prefill + denoise chains (BASELINE config 3); 0 skips")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -418,6 +429,38 @@ def main():
                                   "reference_published_ms": 9.5,
                                   "reference_published_setup": "RTX 5090, fp8 weights, horizon 10 (T=16), LIBERO "
                                                                "prefix, 10 steps (src/pi05/README.md:19)"}
+    if args.fp8_launches > 0:
+        # FP8-W8A16 weights (the reference's pi0.5 numerics): BASELINE shape and the reference's Tv = 10.
+        pk8 = pi05.pack_weights_fp8(w["wq"], w["wk"], w["wv"], w["wo"], w["wg"], w["wu"], w["wd"])
+        fp8 = {"workload": "pi05_expert_bs1_T50_Lp968_S10 with FP8-W8A16 weights (per-row e4m3)"}
+        for tv_, key in ((TV, "T50"), (10, "T10")):
+            c8, s8 = pi05.rope_table(LP, tv_, device=dev)
+            x8 = inp["noise"][0][:tv_].clone()
+
+            def step8():
+                pi05.launch(pk8["w1"], pk8["wo"], pk8["w2"], pk8["w3"], pk8["s1"], pk8["so"], pk8["s2"], pk8["s3"],
+                            mods, modf, c8, s8, w["w_ain"], w["b_ain"], w["w_aout"], w["b_aout"], None, None, 0, kc,
+                            vc, LP, Lmax, S, tv_, x8)
+
+            for _ in range(3):
+                step8()
+            torch.cuda.synchronize()
+            e8 = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            e8[0].record(stream)
+            for _ in range(args.fp8_launches):
+                step8()
+            e8[1].record(stream)
+            torch.cuda.synchronize()
+            ms8 = e8[0].elapsed_time(e8[1]) / args.fp8_launches
+            nb8 = fp8_bytes_per_chunk(tv=tv_)
+            fp8[key] = {"ms_per_chunk": round(ms8, 3), "algorithmic_bytes": nb8,
+                        "roofline": {"bound": "hbm", "achieved": round(nb8 / (ms8 * 1e-3) / 1e9, 1),
+                                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                     "frac": round(nb8 / (ms8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+        fp8["T10"]["reference_published_ms"] = 9.5
+        fp8["kernel_status"] = pi05.read_status(pi05.workspace(dev))
+        res["fp8"] = fp8
+        del pk8
     if args.prefill_launches > 0:
         kc3, vc3 = torch.zeros_like(kc), torch.zeros_like(vc)
         x3 = inp["noise"][0].clone()

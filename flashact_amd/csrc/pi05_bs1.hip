@@ -44,8 +44,17 @@ constexpr int D = 1024, HD = 256, AD = 32;
 constexpr int NX = 8, NR = 32, NWG = 256, TP = 64;
 constexpr int NCW = 4, NLW = 2, NTH = 64 * (NCW + NLW);  // compute waves, loader waves
 constexpr int NCH = 32;                                 // attention key chunks per head
-constexpr int RING = 9, PAGE = 16384, PPL = 13;         // ring pages, page bytes, pages per layer
-constexpr int PG_QKV = 0, PG_K = 4, PG_V = 5, PG_O = 6, PG_GU = 7, PG_DN = 11;
+constexpr int RING = 9, PAGE = 16384;                  // ring pages, page bytes
+// Ring pages of one layer. With bf16 weights a weight page holds 16 fragments of 16 rows x 32 k
+// (1 KB each); with fp8 weights it holds 16 fragment pairs of 16 rows x 64 k (the same 1 KB per
+// copy instruction), so each weight kind needs half the pages. K and V^T pages are bf16 in both.
+template <bool FP8>
+struct Pages {
+  static constexpr int QKV = 0, NQKV = FP8 ? 2 : 4;
+  static constexpr int K = QKV + NQKV, V = K + 1, O = V + 1, GU = O + 1, NGU = FP8 ? 2 : 4;
+  static constexpr int DN = GU + NGU, NDN = FP8 ? 1 : 2, PPL = DN + NDN;
+};
+constexpr int PPL_MAX = Pages<false>::PPL;
 constexpr int MAXF = 1;                                 // pages in flight per loader wave
 constexpr uint32_t OOB = 0x80000000u;                   // buffer offset past every resource
 
@@ -85,10 +94,14 @@ __host__ __device__ constexpr uint32_t frag_off(int KS, int t, int k) {
 }
 
 struct Params {
-  const bf16* w1;
+  const bf16* w1;  // bf16 weights, or e4m3 codes (fp8 launch) at the same addresses
   const bf16* wo;
   const bf16* w2;
   const bf16* w3;
+  const float* s1;  // fp8 launch: per-row scales of the packed rows of w1, wo, w2, w3
+  const float* so;
+  const float* s2;
+  const float* s3;
   const float* mods;
   const float* mod_final;
   const float* rope_cos;
@@ -203,45 +216,63 @@ __device__ __forceinline__ int qkv_row(int g, int vr) {
 //   6   O    (F: row tile F/8, k-step F%8) of W_o[32r.., 256g..]
 //   7-10 GU  (F = 16(i-7) + f: row tile F/32, k-step F%32)
 //   11-12 DN (F = 16(i-11) + f: row tile F/16, k-step F%16)
-// Within one wave's half page, fragment ff (0..7) of every kind sits at a fixed byte stride from
-// fragment 0, and layer l at a fixed stride from layer 0, so each lane precomputes one base
-// address per page kind. Lanes whose rows this CU does not use copy a row it does (QKV tile 1
+// (fp8 weights: see loader_bases.) Within one wave's half page, fragment ff (0..7) of every kind
+// sits at a fixed byte stride from fragment 0, and layer l at a fixed stride from layer 0, so each
+// lane precomputes one base address per page kind. Lanes whose rows this CU does not use copy a row it does (QKV tile 1
 // lanes 8-15, keys past the prefix), so every copy runs with a full exec mask.
 struct LoaderBases {
-  const unsigned char* b[PPL];
+  const unsigned char* b[PPL_MAX];
 };
 
+// fp8 pages: QKV / GU page i = row tile i, slot = pair of k-steps (loader wave lw copies pairs
+// 8lw..8lw+7); O and DN: row tile lw, slot 8lw + pair (O has 4 pairs per row tile: slots
+// 8lw+4..8lw+7 repeat 8lw..8lw+3 so every page is 16 copies). A lane copies 16 bytes of its row.
+template <bool FP8>
 __device__ __forceinline__ void loader_bases(const Params& p, const Ctx& c, int lw, LoaderBases& L) {
+  using P = Pages<FP8>;
+  const unsigned char* w1 = reinterpret_cast<const unsigned char*>(p.w1);
+  const unsigned char* wo = reinterpret_cast<const unsigned char*>(p.wo);
+  const unsigned char* w2 = reinterpret_cast<const unsigned char*>(p.w2);
+  const unsigned char* w3 = reinterpret_cast<const unsigned char*>(p.w3);
+  if constexpr (FP8) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int F0 = 16 * i + 8 * lw, rt = F0 >> 5, ks0 = F0 & 31;
-    const int lr = (rt == 1 && c.lr >= 8) ? c.lr - 8 : c.lr;
-    L.b[i] = reinterpret_cast<const unsigned char*>(p.w1 + (size_t)qkv_row(c.g, 24 * c.r + rt * 16 + lr) * D +
-                                                    ks0 * 32 + c.lq * 8);
+    for (int i = 0; i < P::NQKV; i++) {
+      const int lr = (i == 1 && c.lr >= 8) ? c.lr - 8 : c.lr;
+      L.b[P::QKV + i] = w1 + (size_t)qkv_row(c.g, 24 * c.r + i * 16 + lr) * D + 512 * lw + 16 * c.lq;
+    }
+    L.b[P::O] = wo + (size_t)(32 * c.r + 16 * lw + c.lr) * 2048 + 256 * c.g + 16 * c.lq;
+#pragma unroll
+    for (int i = 0; i < P::NGU; i++)
+      L.b[P::GU + i] = w2 + (size_t)(1024 * c.g + 32 * c.r + 16 * i + c.lr) * D + 512 * lw + 16 * c.lq;
+    L.b[P::DN] = w3 + (size_t)(32 * c.r + 16 * lw + c.lr) * 4096 + 512 * c.g + 16 * c.lq;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int F0 = 16 * i + 8 * lw, rt = F0 >> 5, ks0 = F0 & 31;
+      const int lr = (rt == 1 && c.lr >= 8) ? c.lr - 8 : c.lr;
+      L.b[i] = w1 + ((size_t)qkv_row(c.g, 24 * c.r + rt * 16 + lr) * D + ks0 * 32 + c.lq * 8) * 2;
+    }
+    L.b[P::O] = wo + ((size_t)(32 * c.r + 16 * lw + c.lr) * 2048 + 256 * c.g + c.lq * 8) * 2;
+#pragma unroll
+    for (int i = P::GU; i < P::DN; i++) {
+      const int F0 = 16 * (i - P::GU) + 8 * lw, rt = F0 >> 5, ks0 = F0 & 31;
+      L.b[i] = w2 + ((size_t)(1024 * c.g + 32 * c.r + 16 * rt + c.lr) * D + ks0 * 32 + c.lq * 8) * 2;
+    }
+#pragma unroll
+    for (int i = P::DN; i < P::PPL; i++)
+      L.b[i] = w3 + ((size_t)(32 * c.r + 16 * (i - P::DN) + c.lr) * 4096 + 512 * c.g + 8 * lw * 32 + c.lq * 8) * 2;
   }
   {
     int key = c.kb0 + 16 * lw + c.lr;
     if (key >= p.Lp) key = 0;
-    L.b[PG_K] = reinterpret_cast<const unsigned char*>(p.kcache + (size_t)key * HD + c.lq * 8);
+    L.b[P::K] = reinterpret_cast<const unsigned char*>(p.kcache + (size_t)key * HD + c.lq * 8);
     // An 8-key group that starts inside the prefix is copied from its own row even when it runs
     // past Lp (it stays inside the row: Lmax >= 8 * ceil(Lp / 8)); keys >= Lp are masked by the
     // attention stage. Groups entirely past the prefix copy keys 0..7 instead.
     int kv = c.kb0 + 8 * c.lq;
     if (kv >= p.Lp) kv = 0;
-    L.b[PG_V] = reinterpret_cast<const unsigned char*>(p.vtcache + (size_t)(128 * lw + c.lr) * p.Lmax + kv);
+    L.b[P::V] = reinterpret_cast<const unsigned char*>(p.vtcache + (size_t)(128 * lw + c.lr) * p.Lmax + kv);
   }
-  L.b[PG_O] = reinterpret_cast<const unsigned char*>(p.wo + (size_t)(32 * c.r + 16 * lw + c.lr) * 2048 + 256 * c.g +
-                                                     c.lq * 8);
-#pragma unroll
-  for (int i = PG_GU; i < PG_DN; i++) {
-    const int F0 = 16 * (i - PG_GU) + 8 * lw, rt = F0 >> 5, ks0 = F0 & 31;
-    L.b[i] = reinterpret_cast<const unsigned char*>(p.w2 + (size_t)(1024 * c.g + 32 * c.r + 16 * rt + c.lr) * D +
-                                                    ks0 * 32 + c.lq * 8);
-  }
-#pragma unroll
-  for (int i = PG_DN; i < PPL; i++)
-    L.b[i] = reinterpret_cast<const unsigned char*>(p.w3 + (size_t)(32 * c.r + 16 * (i - PG_DN) + c.lr) * 4096 +
-                                                    512 * c.g + 8 * lw * 32 + c.lq * 8);
 }
 
 #define FA_VMCNT(n) (((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
@@ -263,9 +294,13 @@ __device__ __forceinline__ void vm_wait_pages(int n) {
 // (every compute wave has released page pg - RING) and fewer than MAXF pages of this wave in
 // flight. While it cannot issue, the wave completes its oldest page and publishes
 // ready[lw] = number of pages landed. Ends when every page has landed (or on abort).
+template <bool FP8>
 __device__ void loader_main(const Params& p, const Ctx& c, int lw) {
+  using P = Pages<FP8>;
+  constexpr int PPL = P::PPL;
+  constexpr size_t EB = FP8 ? 1 : 2;  // bytes per weight element
   LoaderBases L;
-  loader_bases(p, c, lw, L);
+  loader_bases<FP8>(p, c, lw, L);
   const int NL = p.NL;
   const int total = p.S * NL * PPL;
   const size_t kvl = (size_t)p.Lmax * HD * 2;  // layer stride of both caches (bytes)
@@ -312,16 +347,17 @@ __device__ void loader_main(const Params& p, const Ctx& c, int lw) {
         __builtin_amdgcn_s_sleep(2);
       }
       if (!ok) break;
-      const size_t lstride = i < PG_K ? (size_t)2560 * D * 2
-                           : i <= PG_V ? kvl
-                           : i == PG_O ? (size_t)D * 2048 * 2
-                           : i < PG_DN ? (size_t)8192 * D * 2
-                                       : (size_t)D * 4096 * 2;
-      const uint32_t fstride = i == PG_V ? vfs : 64u;
+      const size_t lstride = i < P::K ? (size_t)2560 * D * EB
+                           : i <= P::V ? kvl
+                           : i == P::O ? (size_t)D * 2048 * EB
+                           : i < P::DN ? (size_t)8192 * D * EB
+                                       : (size_t)D * 4096 * EB;
+      const uint32_t fstride = i == P::V ? vfs : 64u;
+      const int fmask = (FP8 && i == P::O) ? 3 : 7;  // fp8 O: 4 pairs per row tile, copied twice
       const unsigned char* src = L.b[i] + (size_t)l * lstride;
       const uint32_t dst = c.lds_addr + (uint32_t)(pg % RING) * PAGE + lw * 8 * 1024;
 #pragma unroll
-      for (int ff = 0; ff < 8; ff++) dma16(src + ff * fstride, dst + ff * 1024);
+      for (int ff = 0; ff < 8; ff++) dma16(src + (ff & fmask) * fstride, dst + ff * 1024);
       if (tr && c.lane == 0 && pg >= tpg0 && pg < tpg0 + PPL) tr[2 * (pg - tpg0)] = __builtin_amdgcn_s_memrealtime();
     }
   }
@@ -331,14 +367,27 @@ __device__ void loader_main(const Params& p, const Ctx& c, int lw) {
 }
 
 // ---------------------------------------------------------------- GEMM (one token tile)
-// acc[rt] = sum_k W[row tile rt][k] * X[token 16w+lr][k] over KS k-steps. Weight fragment
-// F = rt*KS + ks is slot F%16 of ring page pg0 + F/16. xoff = byte offset in the workspace of
-// X[token][k = 8 lq] (OOB for tokens >= Tv: the loads return zeros); k-step ks adds XSTRIDE bytes.
-template <int RT, int KS, int XSTRIDE = 64>
+// Eight e4m3 weights (k order in bytes 0..7) -> the eight bf16 of an MFMA operand. e4m3 values
+// are exact in bf16, so the conversion (scale 1) is exact; the row scale is applied to the sums.
+template <bool HI>
+__device__ __forceinline__ unsigned cvt_fp8x2(unsigned w) {
+  return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+}
+__device__ __forceinline__ u32x4 fp8x8_to_bf16(unsigned lo, unsigned hi) {
+  return u32x4{cvt_fp8x2<false>(lo), cvt_fp8x2<true>(lo), cvt_fp8x2<false>(hi), cvt_fp8x2<true>(hi)};
+}
+
+// acc[rt] = sum_k W[row tile rt][k] * X[token 16w+lr][k] over KS k-steps. bf16 weights: fragment
+// F = rt*KS + ks is slot F%16 of ring page pg0 + F/16. fp8 weights: pair P = rt*PRT + ks/2 is slot
+// P%16 of page pg0 + P/16; its 1 KB holds row lr, k 16q..16q+15 of the pair at byte 16 (lr + 16 q),
+// so k-step ks reads 8 bytes at 16 lr + 256 (2 (ks%2) + lq/2) + 8 (lq%2). xoff = byte offset in the
+// workspace of X[token][k = 8 lq] (OOB for tokens >= Tv: the loads return zeros); k-step ks adds
+// XSTRIDE bytes.
+template <int RT, int KS, int XSTRIDE = 64, bool FP8 = false, int PRT = KS / 2>
 __device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0, uint32_t xoff, int ts) {
   // Software-pipelined in chunks of 8 k-steps: the loads of chunk i+1 are in flight while the
   // MFMAs of chunk i run, so compute starts as soon as the first operands arrive.
-  constexpr int NPG = (RT * KS + 15) / 16;
+  constexpr int NPG = FP8 ? (RT * PRT + 15) / 16 : (RT * KS + 15) / 16;
   constexpr int KC = KS < 8 ? KS : 8;
   constexpr int NCK = KS / KC;
   u32x4 xf[2][KC];
@@ -351,8 +400,9 @@ __device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0
   page_wait(c, pg0 + NPG - 1);
   stamp(c, ts);
   uint32_t slot[NPG];
+  const uint32_t loff = FP8 ? 16 * c.lr + 256 * (c.lq >> 1) + 8 * (c.lq & 1) : c.lane * 16;
 #pragma unroll
-  for (int k = 0; k < NPG; k++) slot[k] = ((pg0 + k) % RING) * PAGE + c.lane * 16;
+  for (int k = 0; k < NPG; k++) slot[k] = ((pg0 + k) % RING) * PAGE + loff;
 #pragma unroll
   for (int ck = 0; ck < NCK; ck++) {
     if (ck + 1 < NCK) {
@@ -364,8 +414,15 @@ __device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0
     for (int k = 0; k < KC; k++)
 #pragma unroll
       for (int rt = 0; rt < RT; rt++) {
-        const int F = rt * KS + ck * KC + k;
-        const u32x4 a = *reinterpret_cast<const u32x4*>(fa_lds + slot[F >> 4] + (F & 15) * 1024);
+        u32x4 a;
+        if constexpr (FP8) {
+          const int ks = ck * KC + k, P = rt * PRT + (ks >> 1);
+          const u32x2 q = *reinterpret_cast<const u32x2*>(fa_lds + slot[P >> 4] + (P & 15) * 1024 + 512 * (ks & 1));
+          a = fp8x8_to_bf16(q[0], q[1]);
+        } else {
+          const int F = rt * KS + ck * KC + k;
+          a = *reinterpret_cast<const u32x4*>(fa_lds + slot[F >> 4] + (F & 15) * 1024);
+        }
         ac2[rt][k & 1] = mfma16(a, xf[ck & 1][k], ac2[rt][k & 1]);
       }
     __builtin_amdgcn_sched_barrier(0);
@@ -527,7 +584,11 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int bu
   }
 }
 
+// fp8 launch: the scales of four consecutive rows (one lane's output rows of a row tile).
+__device__ __forceinline__ f32x4 row_scales(const float* s, size_t row0) { return *reinterpret_cast<const f32x4*>(s + row0); }
+
 // ---------------------------------------------------------------- QKV
+template <bool FP8>
 __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, int pg0, bool last) {
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
@@ -541,9 +602,23 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
     cs[rt] = ldb64<kCpPlain>(c.rc, o);
     sn[rt] = ldb64<kCpPlain>(c.rs, o);
   }
+  f32x4 sc[2];
+  if constexpr (FP8) {
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+      const int vr0 = (rt == 0 || c.lq < 2) ? 24 * c.r + rt * 16 + 4 * c.lq : 0;  // rows of this rank only
+      sc[rt] = row_scales(p.s1, (size_t)l * 2560 + qkv_row(c.g, vr0));
+    }
+  }
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  if (any) gemm_tok<2, 32, 1024>(acc, c, pg0, tv ? OFF_XN + c.g * (TP * D * 2) + frag_off(32, t, 8 * c.lq) : OOB, 15);
-  page_release(c, pg0 + 4);
+  if (any)
+    gemm_tok<2, 32, 1024, FP8, 16>(acc, c, pg0, tv ? OFF_XN + c.g * (TP * D * 2) + frag_off(32, t, 8 * c.lq) : OOB,
+                                   15);
+  page_release(c, pg0 + Pages<FP8>::NQKV);
+  if constexpr (FP8) {
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) acc[rt] *= sc[rt];
+  }
 #pragma unroll
   for (int rt = 0; rt < 2; rt++) {
     if (rt == 1 && c.lq >= 2) continue;  // rows 24r+24.. belong to the next rank
@@ -807,13 +882,23 @@ __device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c) {
 // ---------------------------------------------------------------- O projection (K-window g)
 // Writes all 16 token slots of the tile (zeros past Tv) so every exchange slot carries the
 // current parity.
-__device__ __forceinline__ void stage_oproj(const Params& p, const Ctx& c, int pg, unsigned par) {
+template <bool FP8>
+__device__ __forceinline__ void stage_oproj(const Params& p, const Ctx& c, int l, int pg, unsigned par) {
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
+  f32x4 sc[2];
+  if constexpr (FP8) {
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) sc[rt] = row_scales(p.so, (size_t)l * D + 32 * c.r + rt * 16 + 4 * c.lq);
+  }
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
   if (16 * c.wave < p.Tv)
-    gemm_tok<2, 8, 1024>(acc, c, pg, tv ? OFF_ATTN + c.g * (TP * HD * 2) + frag_off(8, t, 8 * c.lq) : OOB, 17);
+    gemm_tok<2, 8, 1024, FP8, 8>(acc, c, pg, tv ? OFF_ATTN + c.g * (TP * HD * 2) + frag_off(8, t, 8 * c.lq) : OOB, 17);
   page_release(c, pg + 1);
+  if constexpr (FP8) {
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) acc[rt] *= sc[rt];
+  }
 #pragma unroll
   for (int rt = 0; rt < 2; rt++)
     stb128<kCpSc1>(c.ws, OFF_XP + (((0 * NX + c.g) * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 4,
@@ -821,17 +906,29 @@ __device__ __forceinline__ void stage_oproj(const Params& p, const Ctx& c, int p
 }
 
 // ---------------------------------------------------------------- gate/up (F-slice g)
-__device__ __forceinline__ void stage_gu(const Params& p, const Ctx& c, int pg0) {
+template <bool FP8>
+__device__ __forceinline__ void stage_gu(const Params& p, const Ctx& c, int l, int pg0) {
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
   if (16 * c.wave >= p.Tv) {
-    page_release(c, pg0 + 4);
+    page_release(c, pg0 + Pages<FP8>::NGU);
     return;
   }
+  f32x4 sc[2];
+  if constexpr (FP8) {
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+      sc[rt] = row_scales(p.s2, (size_t)l * 8192 + 1024 * c.g + 32 * c.r + rt * 16 + 4 * c.lq);
+  }
   f32x4 acc[2];
-  gemm_tok<2, 32, 1024>(acc, c, pg0, tv ? OFF_XN + c.g * (TP * D * 2) + frag_off(32, t, 8 * c.lq) : OOB, 19);
-  page_release(c, pg0 + 4);
+  gemm_tok<2, 32, 1024, FP8, 16>(acc, c, pg0, tv ? OFF_XN + c.g * (TP * D * 2) + frag_off(32, t, 8 * c.lq) : OOB,
+                                 19);
+  page_release(c, pg0 + Pages<FP8>::NGU);
   if (!tv) return;
+  if constexpr (FP8) {
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) acc[rt] *= sc[rt];
+  }
   // h(f) = gelu(gate f) * up f for this CU's 16 columns f = 8rt + 2lq + (0, 1). One exchange with
   // lane ^ 16 gives every lane 4 consecutive columns, written as 8 bytes of the fragment-ordered h.
   const unsigned p0 = pack_bf16x2(gelu_tanh(acc[0][0]) * acc[0][1], gelu_tanh(acc[0][2]) * acc[0][3]);
@@ -844,13 +941,24 @@ __device__ __forceinline__ void stage_gu(const Params& p, const Ctx& c, int pg0)
 }
 
 // ---------------------------------------------------------------- down (K-window g)
-__device__ __forceinline__ void stage_dn(const Params& p, const Ctx& c, int pg0, unsigned par) {
+template <bool FP8>
+__device__ __forceinline__ void stage_dn(const Params& p, const Ctx& c, int l, int pg0, unsigned par) {
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
+  f32x4 sc[2];
+  if constexpr (FP8) {
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) sc[rt] = row_scales(p.s3, (size_t)l * D + 32 * c.r + rt * 16 + 4 * c.lq);
+  }
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
   if (16 * c.wave < p.Tv)
-    gemm_tok<2, 16, 1024>(acc, c, pg0, tv ? OFF_H + c.g * (TP * 512 * 2) + frag_off(16, t, 8 * c.lq) : OOB, 21);
-  page_release(c, pg0 + 2);
+    gemm_tok<2, 16, 1024, FP8, 8>(acc, c, pg0, tv ? OFF_H + c.g * (TP * 512 * 2) + frag_off(16, t, 8 * c.lq) : OOB,
+                                  21);
+  page_release(c, pg0 + Pages<FP8>::NDN);
+  if constexpr (FP8) {
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) acc[rt] *= sc[rt];
+  }
 #pragma unroll
   for (int rt = 0; rt < 2; rt++)
     stb128<kCpSc1>(c.ws, OFF_XP + (((1 * NX + c.g) * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 4,
@@ -867,7 +975,9 @@ __device__ __forceinline__ void mark(const Params& p, const Ctx& c, int idx, uin
 }
 
 // ---------------------------------------------------------------- kernel
+template <bool FP8>
 __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
+  using PG = Pages<FP8>;
   Ctx c;
   const int tid = threadIdx.x;
   c.lane = tid & 63;
@@ -894,7 +1004,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       __hip_atomic_load(reinterpret_cast<const unsigned*>(p.ws + kWsOwner), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();  // the only workgroup barrier: LDS control words are initialised
   if (c.wave >= NCW) {
-    loader_main(p, c, c.wave - NCW);
+    loader_main<FP8>(p, c, c.wave - NCW);
     return;
   }
   c.e = seq << 32;
@@ -929,7 +1039,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       // loop instead of hoisting hundreds of loop-invariant offsets (which spill).
       asm volatile("" : "+v"(c.lane), "+v"(c.lr), "+v"(c.lq));
       const int li = step * NL + l;
-      const int pb = li * PPL;
+      const int pb = li * PG::PPL;
       const unsigned par = (1u + xbase + (unsigned)li) & 1u;
       c.tr = (p.trace && li == p.trace_layer) ? p.trace + ((size_t)blockIdx.x * (NCW + 2) + c.wave) * 32 : nullptr;
       const float* mod_in = p.mods + ((size_t)li * 2 + 0) * 3 * D;
@@ -946,13 +1056,13 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       xcd_sync(p, c);
       mark(p, c, 9, t0);
       stamp(c, 2);
-      stage_qkv(p, c, l, pb + PG_QKV, step == p.S - 1);
+      stage_qkv<FP8>(p, c, l, pb + PG::QKV, step == p.S - 1);
       stamp(c, 3);
       mark(p, c, 1, t0);
       xcd_sync(p, c);
       mark(p, c, 9, t0);
       stamp(c, 4);
-      stage_att(p, c, l, pb + PG_K);
+      stage_att(p, c, l, pb + PG::K);
       stamp(c, 5);
       mark(p, c, 2, t0);
       xcd_sync(p, c);
@@ -964,7 +1074,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       xcd_sync(p, c);
       mark(p, c, 9, t0);
       stamp(c, 8);
-      stage_oproj(p, c, pb + PG_O, par);
+      stage_oproj<FP8>(p, c, l, pb + PG::O, par);
       stamp(c, 9);
       mark(p, c, 4, t0);
       if (nw) stage_norm<1>(p, c, 0, par, mod_in + 2 * D, mod_post, mod_post + D, 0.f);
@@ -973,13 +1083,13 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       xcd_sync(p, c);
       mark(p, c, 9, t0);
       stamp(c, 11);
-      stage_gu(p, c, pb + PG_GU);
+      stage_gu<FP8>(p, c, l, pb + PG::GU);
       stamp(c, 12);
       mark(p, c, 6, t0);
       xcd_sync(p, c);
       mark(p, c, 9, t0);
       stamp(c, 13);
-      stage_dn(p, c, pb + PG_DN, par);
+      stage_dn<FP8>(p, c, l, pb + PG::DN, par);
       stamp(c, 14);
       mark(p, c, 7, t0);
     }
@@ -1043,11 +1153,22 @@ extern "C" int fa_pi05_read_status(const void* workspace, unsigned* status) {
 extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
   using namespace fa::pi05;
   if (!a) return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: args is NULL");
-  if (a->weight_dtype != FA_DTYPE_BF16)
-    return host::fail(FA_ERR_UNSUPPORTED, "fa_pi05_denoise: only bf16 weights are implemented (weight_dtype=%d)",
-                      a->weight_dtype);
-  if (a->s1 || a->so || a->s2 || a->s3)
+  const bool fp8 = a->weight_dtype == FA_DTYPE_FP8_E4M3;
+  if (!fp8 && a->weight_dtype != FA_DTYPE_BF16)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: unknown weight_dtype=%d", a->weight_dtype);
+  if (!fp8 && (a->s1 || a->so || a->s2 || a->s3))
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: fp8 row scales must be NULL for bf16 weights");
+  if (fp8) {
+    if (a->batch != 1)
+      return host::fail(FA_ERR_UNSUPPORTED, "fa_pi05_denoise: fp8 weights are implemented for batch 1 (got batch=%d)",
+                        a->batch);
+    const float* sc[] = {a->s1, a->so, a->s2, a->s3};
+    for (const float* x : sc) {
+      if (!x) return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: fp8 weights need the row scales s1, so, s2, s3");
+      if (reinterpret_cast<uintptr_t>(x) & 15)
+        return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: fp8 row scales must be 16-byte aligned");
+    }
+  }
   if (a->srows < 0) return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: srows=%d < 0", a->srows);
   if (a->srows > 0) {  // K/V hand-off from a prefill's cache rows (src/pi05/mk6.cu:258-277)
     if (!a->kvsrc_k || !a->kvsrc_v)
@@ -1086,7 +1207,8 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
   if (a->workspace_bytes < WS_BYTES)
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: workspace_bytes=%zu < required %u", a->workspace_bytes,
                       (unsigned)WS_BYTES);
-  int rc = host::check_device((const void*)pi05_denoise_bs1, NTH, LDS_BYTES, NWG, "fa_pi05_denoise");
+  const void* kern = fp8 ? (const void*)pi05_denoise_bs1<true> : (const void*)pi05_denoise_bs1<false>;
+  int rc = host::check_device(kern, NTH, LDS_BYTES, NWG, "fa_pi05_denoise");
   if (rc != FA_OK) return rc;
 
   Params p;
@@ -1094,6 +1216,10 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
   p.wo = static_cast<const bf16*>(a->wo);
   p.w2 = static_cast<const bf16*>(a->w2);
   p.w3 = static_cast<const bf16*>(a->w3);
+  p.s1 = a->s1;
+  p.so = a->so;
+  p.s2 = a->s2;
+  p.s3 = a->s3;
   p.mods = a->mods;
   p.mod_final = a->mod_final;
   p.rope_cos = a->rope_cos;
@@ -1117,7 +1243,7 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
   p.xt_rows = a->xt_rows;
   if (a->srows > 0 && (rc = pi05_kv_handoff(a, stream)) != FA_OK) return rc;
   void* args[] = {&p};
-  hipError_t e = hipLaunchCooperativeKernel((const void*)pi05_denoise_bs1, dim3(NWG), dim3(NTH), args, LDS_BYTES,
+  hipError_t e = hipLaunchCooperativeKernel(kern, dim3(NWG), dim3(NTH), args, LDS_BYTES,
                                             (hipStream_t)stream);
   if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_pi05_denoise: cooperative launch failed: %s",
                                          hipGetErrorString(e));

@@ -51,6 +51,26 @@ def pack_weights(wq, wk, wv, wo, wg, wu, wd):
     return {"w1": w1, "wo": wo.to(bf).contiguous(), "w2": w2, "w3": wd.to(bf).contiguous()}
 
 
+def quantize_fp8(w: torch.Tensor):
+    """Per-row FP8 (OCP E4M3) quantisation, the reference's (src/pi05/hybrid_model.py:105-110):
+    s = max|w| / 448 over the row (at least 1e-8), q = e4m3(clamp(w / s, +-448)). Returns (codes
+    uint8 [..][N][K], scales fp32 [..][N])."""
+    s = w.float().abs().amax(dim=-1).clamp(min=1e-8) / 448.0
+    q = (w.float() / s[..., None]).clamp(-448, 448).to(torch.float8_e4m3fn)
+    return q.view(torch.uint8).contiguous(), s.float().contiguous()
+
+
+def pack_weights_fp8(wq, wk, wv, wo, wg, wu, wd):
+    """pack_weights, then per-row FP8 quantisation of each packed buffer (the reference quantises the
+    packed rows; a row keeps its values under the packing permutation). Returns w1 wo w2 w3 (uint8
+    codes) and s1 so s2 s3 (fp32 row scales)."""
+    p = pack_weights(wq, wk, wv, wo, wg, wu, wd)
+    out = {}
+    for k, sk in (("w1", "s1"), ("wo", "so"), ("w2", "s2"), ("w3", "s3")):
+        out[k], out[sk] = quantize_fp8(p[k])
+    return out
+
+
 def create_sinusoidal_pos_embedding(time: torch.Tensor, dimension: int, min_period: float = 4e-3,
                                     max_period: float = 4.0) -> torch.Tensor:
     """Sine/cosine time embedding [n, dimension]: fraction = linspace(0, 1, dim/2) in fp64,
@@ -173,8 +193,9 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
     """Runs the whole ``num_steps`` Euler loop; ``x_t`` is updated in place (the output).
 
     Same positional order as the reference ``launch``. Differences, all by design:
-      * weights are bf16 ([NL][2560][1024] ... as packed by ``pack_weights``); s1..s3 must be
-        empty/None (fp8 row scales are for the fp8 weight mode, not implemented here);
+      * weights are bf16 ([NL][2560][1024] ... as packed by ``pack_weights``) with s1..s3 empty/None,
+        or FP8-W8A16 (batch 1): e4m3 codes (uint8 or float8_e4m3fn) with fp32 per-row scales s1..s3,
+        as ``pack_weights_fp8`` makes them (the reference's quantisation);
       * kcache/vtcache are bf16 (the reference used fp16);
       * the scratch tensors x, xp, xn, q, attn, hmlp, scores, probs are accepted and ignored: the
         MI355X engine keeps its intermediates in one workspace (``workspace()``);
@@ -185,10 +206,13 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
     L = _lib.lib()
     if w1.dtype == torch.bfloat16:
         wdt = _lib.FA_DTYPE_BF16
-    elif w1.dtype == torch.uint8:
+    elif w1.dtype in (torch.uint8, torch.float8_e4m3fn):
         wdt = _lib.FA_DTYPE_FP8_E4M3
+        for name, t in (("s1", s1), ("so", so_), ("s2", s2), ("s3", s3)):
+            if t is None or t.dtype != torch.float32:
+                raise TypeError(f"fp8 weights need float32 row scales; {name} is {None if t is None else t.dtype}")
     else:
-        raise TypeError(f"w1 must be bfloat16 (or uint8 fp8), got {w1.dtype}")
+        raise TypeError(f"w1 must be bfloat16, or uint8 / float8_e4m3fn codes, got {w1.dtype}")
     for name, t in (("wo", wo), ("w2", w2), ("w3", w3)):
         if t.dtype != w1.dtype:
             raise TypeError(f"{name} dtype {t.dtype} differs from w1 {w1.dtype}")

@@ -15,6 +15,8 @@
  *       time embedding / time MLP / mods ........ src/pi05/hybrid_model.py:111-128,
  *                                                 src/pi05/pack_weights.py:23-31
  *       RoPE table .............................. src/pi05/pack_weights.py:54-58
+ *       FP8-W8A16 weights (fo_pi05_denoise_fp8) . e4m3 codes + per-row scales (hybrid_model.py:105-110),
+ *                                                 row sum times scale (mk6.cu:204-225)
  *   MolmoAct2 action expert ..................... src/molmoact2/mk_ma2.cu:258-575
  *       adaLN norm ............................... src/molmoact2/mk_ma2.cu:130-158
  *       self-attn qk-norm + RoPE (48 pairs) ..... src/molmoact2/mk_ma2.cu:292-381
@@ -88,6 +90,51 @@ static void linear_f32(const float* X, int M, int K, const float* W, const float
   for (int n = 0; n < N; n++) {
     float b = bias ? bias[n] : 0.f;
     for (int m = 0; m < M; m++) Y[(size_t)m * N + n] = dot_f32(X + (size_t)m * K, W + (size_t)n * K, K) + b;
+  }
+}
+
+/* OCP E4M3 (e4m3fn): e == 0 -> m 2^-9, else (1 + m/8) 2^(e-7); codes 0x7f / 0xff are NaN. */
+static inline float e4m3(uint8_t c) {
+  const int e = (c >> 3) & 15, m = c & 7;
+  float v;
+  if (e == 15 && m == 7)
+    v = NAN;
+  else if (e == 0)
+    v = ldexpf((float)m, -9);
+  else
+    v = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+  return (c & 0x80) ? -v : v;
+}
+
+void fo_e4m3_decode(const uint8_t* codes, int n, float* out) {
+  for (int i = 0; i < n; i++) out[i] = e4m3(codes[i]);
+}
+
+/* A stack of weight matrices [..][N][K]: bf16 bits, or e4m3 codes with one fp32 scale per row. */
+typedef struct {
+  const uint16_t* bf;
+  const uint8_t* q;
+  const float* s;
+} fo_wmat;
+
+/* Y[m][n] = sum_k X[m][k] W[row0 + n][k]; for e4m3 weights the row sum is multiplied by the row's
+ * scale afterwards, (sum_k x_k q_nk) s_n, as the reference's W8A16 GEMM does (mk6.cu:204-225). */
+static void linear_w(const float* X, int M, int K, fo_wmat W, size_t row0, int N, float* Y) {
+  if (!W.q) {
+    linear_bf16(X, M, K, W.bf + row0 * (size_t)K, NULL, N, Y);
+    return;
+  }
+#pragma omp parallel
+  {
+    float* wrow = (float*)malloc(sizeof(float) * (size_t)K);
+#pragma omp for schedule(static)
+    for (int n = 0; n < N; n++) {
+      const uint8_t* w = W.q + (row0 + (size_t)n) * K;
+      for (int k = 0; k < K; k++) wrow[k] = e4m3(w[k]);
+      const float sc = W.s[row0 + n];
+      for (int m = 0; m < M; m++) Y[(size_t)m * N + n] = dot_f32(X + (size_t)m * K, wrow, K) * sc;
+    }
+    free(wrow);
   }
 }
 
@@ -189,11 +236,10 @@ typedef struct {
  * w_ain [D][AD], b_ain [D], w_aout [AD][D], b_aout [AD] (fp32)
  * kpre, vpre [batch][NL][Lp][HD] bf16 (already-RoPE'd prefix keys, values)
  * x_t [batch][Tv][AD] fp32, updated in place. */
-int fo_pi05_denoise(const fo_pi05_dims* dm, const uint16_t* wq, const uint16_t* wk, const uint16_t* wv,
-                    const uint16_t* wo, const uint16_t* wg, const uint16_t* wu, const uint16_t* wd,
-                    const float* mods, const float* mod_final, const float* rope_cos, const float* rope_sin,
-                    const float* w_ain, const float* b_ain, const float* w_aout, const float* b_aout,
-                    const uint16_t* kpre, const uint16_t* vpre, float* x_t) {
+static int pi05_loop(const fo_pi05_dims* dm, fo_wmat wq, fo_wmat wk, fo_wmat wv, fo_wmat wo, fo_wmat wg, fo_wmat wu,
+                     fo_wmat wd, const float* mods, const float* mod_final, const float* rope_cos,
+                     const float* rope_sin, const float* w_ain, const float* b_ain, const float* w_aout,
+                     const float* b_aout, const uint16_t* kpre, const uint16_t* vpre, float* x_t) {
   const int NL = dm->NL, D = dm->D, H = dm->H, HD = dm->HD, F = dm->F, AD = dm->AD;
   const int Lp = dm->Lp, Tv = dm->Tv, S = dm->S, B = dm->batch;
   const int QD = H * HD, half = HD / 2, L = Lp + Tv;
@@ -224,9 +270,9 @@ int fo_pi05_denoise(const fo_pi05_dims* dm, const uint16_t* wq, const uint16_t* 
         const float* mod_post = mods + (((size_t)s * NL + l) * 2 + 1) * 3 * D;
         /* attention block */
         ada_rms(x, Tv, D, mod_in, mod_in + D, h);
-        linear_bf16(h, Tv, D, wq + (size_t)l * QD * D, NULL, QD, q);
-        linear_bf16(h, Tv, D, wk + (size_t)l * HD * D, NULL, HD, k);
-        linear_bf16(h, Tv, D, wv + (size_t)l * HD * D, NULL, HD, v);
+        linear_w(h, Tv, D, wq, (size_t)l * QD, QD, q);
+        linear_w(h, Tv, D, wk, (size_t)l * HD, HD, k);
+        linear_w(h, Tv, D, wv, (size_t)l * HD, HD, v);
         for (int t = 0; t < Tv; t++) {
           const float* c = rope_cos + (size_t)t * half;
           const float* sn = rope_sin + (size_t)t * half;
@@ -269,15 +315,15 @@ int fo_pi05_denoise(const fo_pi05_dims* dm, const uint16_t* wq, const uint16_t* 
           }
           free(p);
         }
-        linear_bf16(att, Tv, QD, wo + (size_t)l * D * QD, NULL, D, o);
+        linear_w(att, Tv, QD, wo, (size_t)l * D, D, o);
         for (int t = 0; t < Tv; t++)
           for (int d = 0; d < D; d++) x[(size_t)t * D + d] += mod_in[2 * D + d] * o[(size_t)t * D + d];
         /* MLP block */
         ada_rms(x, Tv, D, mod_post, mod_post + D, h);
-        linear_bf16(h, Tv, D, wg + (size_t)l * F * D, NULL, F, g);
-        linear_bf16(h, Tv, D, wu + (size_t)l * F * D, NULL, F, u);
+        linear_w(h, Tv, D, wg, (size_t)l * F, F, g);
+        linear_w(h, Tv, D, wu, (size_t)l * F, F, u);
         for (size_t i = 0; i < (size_t)Tv * F; i++) g[i] = gelu_tanh_f(g[i]) * u[i];
-        linear_bf16(g, Tv, F, wd + (size_t)l * D * F, NULL, D, o);
+        linear_w(g, Tv, F, wd, (size_t)l * D, D, o);
         for (int t = 0; t < Tv; t++)
           for (int d = 0; d < D; d++) x[(size_t)t * D + d] += mod_post[2 * D + d] * o[(size_t)t * D + d];
       }
@@ -291,6 +337,32 @@ int fo_pi05_denoise(const fo_pi05_dims* dm, const uint16_t* wq, const uint16_t* 
   free(x); free(h); free(q); free(k); free(v); free(att); free(o); free(g); free(u);
   free(Kl); free(Vl); free(act);
   return 0;
+}
+
+int fo_pi05_denoise(const fo_pi05_dims* dm, const uint16_t* wq, const uint16_t* wk, const uint16_t* wv,
+                    const uint16_t* wo, const uint16_t* wg, const uint16_t* wu, const uint16_t* wd,
+                    const float* mods, const float* mod_final, const float* rope_cos, const float* rope_sin,
+                    const float* w_ain, const float* b_ain, const float* w_aout, const float* b_aout,
+                    const uint16_t* kpre, const uint16_t* vpre, float* x_t) {
+  const fo_wmat W[7] = {{wq, NULL, NULL}, {wk, NULL, NULL}, {wv, NULL, NULL}, {wo, NULL, NULL},
+                        {wg, NULL, NULL}, {wu, NULL, NULL}, {wd, NULL, NULL}};
+  return pi05_loop(dm, W[0], W[1], W[2], W[3], W[4], W[5], W[6], mods, mod_final, rope_cos, rope_sin, w_ain, b_ain,
+                   w_aout, b_aout, kpre, vpre, x_t);
+}
+
+/* FP8-W8A16 weights (the reference's pi0.5 numerics, hybrid_model.py:105-110): e4m3 codes in the
+ * same natural layouts plus one fp32 scale per row, sq [NL][H*HD], sk / sv [NL][HD], so [NL][D],
+ * sg / su [NL][F], sd [NL][D]. */
+int fo_pi05_denoise_fp8(const fo_pi05_dims* dm, const uint8_t* qq, const float* sq, const uint8_t* qk,
+                        const float* sk, const uint8_t* qv, const float* sv, const uint8_t* qo, const float* so,
+                        const uint8_t* qg, const float* sg, const uint8_t* qu, const float* su, const uint8_t* qd,
+                        const float* sd, const float* mods, const float* mod_final, const float* rope_cos,
+                        const float* rope_sin, const float* w_ain, const float* b_ain, const float* w_aout,
+                        const float* b_aout, const uint16_t* kpre, const uint16_t* vpre, float* x_t) {
+  const fo_wmat W[7] = {{NULL, qq, sq}, {NULL, qk, sk}, {NULL, qv, sv}, {NULL, qo, so},
+                        {NULL, qg, sg}, {NULL, qu, su}, {NULL, qd, sd}};
+  return pi05_loop(dm, W[0], W[1], W[2], W[3], W[4], W[5], W[6], mods, mod_final, rope_cos, rope_sin, w_ain, b_ain,
+                   w_aout, b_aout, kpre, vpre, x_t);
 }
 
 /* ------------------------------------------------------------------ */

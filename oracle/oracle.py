@@ -49,6 +49,7 @@ def lib():
         _lib.fo_pi05_denoise.restype = ctypes.c_int
         _lib.fo_ma2_flow.restype = ctypes.c_int
         _lib.fo_gemma_prefill.restype = ctypes.c_int
+        _lib.fo_pi05_denoise_fp8.restype = ctypes.c_int
     return _lib
 
 
@@ -121,6 +122,39 @@ def pi05_denoise(w: dict, x_t, *, Lp: int, Tv: int, S: int, NL: int, D: int = 10
         _p(u["kpre"], np.uint16), _p(u["vpre"], np.uint16), _p(x, np.float32))
     if rc != 0:
         raise ValueError(f"fo_pi05_denoise rejected the dimensions (rc={rc})")
+    return x
+
+
+def e4m3_decode(codes) -> np.ndarray:
+    """fp32 values of OCP E4M3 codes (uint8)."""
+    c = np.ascontiguousarray(codes, dtype=np.uint8)
+    out = np.empty(c.shape, np.float32)
+    lib().fo_e4m3_decode(_p(c, np.uint8), ctypes.c_int(c.size), _p(out, np.float32))
+    return out
+
+
+def pi05_denoise_fp8(w: dict, x_t, *, Lp: int, Tv: int, S: int, NL: int, D: int = 1024, H: int = 8, HD: int = 256,
+                     F: int = 4096, AD: int = 32) -> np.ndarray:
+    """pi05_denoise with FP8-W8A16 weights: ``w`` holds e4m3 codes qq qk qv qo qg qu qd (uint8,
+    natural layouts) and their per-row fp32 scales sq sk sv so sg su sd, plus the fp32 / bf16 inputs
+    of ``pi05_denoise``."""
+    x = _f32(x_t).copy()
+    B = x.shape[0] if x.ndim == 3 else 1
+    dims = Pi05Dims(NL, D, H, HD, F, AD, Lp, Tv, S, B)
+    q = {k: np.ascontiguousarray(w[k], dtype=np.uint8) for k in ("qq", "qk", "qv", "qo", "qg", "qu", "qd")}
+    sc = {k: _f32(w[k]) for k in ("sq", "sk", "sv", "so", "sg", "su", "sd")}
+    f = {k: _f32(w[k]) for k in ("mods", "mod_final", "rope_cos", "rope_sin", "w_ain", "b_ain", "w_aout", "b_aout")}
+    u = {k: _u16(w[k]) for k in ("kpre", "vpre")}
+    args = []
+    for a, b in (("qq", "sq"), ("qk", "sk"), ("qv", "sv"), ("qo", "so"), ("qg", "sg"), ("qu", "su"), ("qd", "sd")):
+        args += [_p(q[a], np.uint8), _p(sc[b], np.float32)]
+    rc = lib().fo_pi05_denoise_fp8(
+        ctypes.byref(dims), *args,
+        *[_p(f[k], np.float32) for k in ("mods", "mod_final", "rope_cos", "rope_sin", "w_ain", "b_ain", "w_aout",
+                                          "b_aout")],
+        _p(u["kpre"], np.uint16), _p(u["vpre"], np.uint16), _p(x, np.float32))
+    if rc != 0:
+        raise ValueError(f"fo_pi05_denoise_fp8 rejected the dimensions (rc={rc})")
     return x
 
 

@@ -69,7 +69,11 @@ def _args(**kw):
     (dict(srows=900, kvsrc_k=1 << 20, kvsrc_v=1 << 20), 1, "srows=900 < Lp=968"),
     (dict(srows=968, kvsrc_k=(1 << 20) + 2, kvsrc_v=1 << 20), 1, "not 16-byte aligned"),
     (dict(srows=-1), 1, "srows"),
-    (dict(weight_dtype=1), 2, "bf16"),
+    (dict(weight_dtype=1), 1, "row scales"),
+    (dict(weight_dtype=1, s1=1 << 20, so=1 << 20, s2=1 << 20, s3=(1 << 20) + 4), 1, "16-byte aligned"),
+    (dict(weight_dtype=1, s1=1 << 20, so=1 << 20, s2=1 << 20, s3=1 << 20, batch=2), 2, "batch 1"),
+    (dict(weight_dtype=7), 1, "weight_dtype"),
+    (dict(s2=1 << 20), 1, "must be NULL for bf16"),
     (dict(batch=65), 1, "batch"),
     (dict(batch=0), 1, "batch"),
     (dict(batch=16, workspace_bytes=4096), 1, "workspace"),
@@ -93,6 +97,8 @@ def test_denoise_without_device(lib):
         pytest.skip("a GPU is present")
     assert lib.fa_pi05_denoise(ctypes.byref(_args()), None) == 3
     assert lib.fa_pi05_denoise(ctypes.byref(_args(batch=16)), None) == 3
+    fp8 = _args(weight_dtype=1, s1=1 << 20, so=1 << 20, s2=1 << 20, s3=1 << 20)
+    assert lib.fa_pi05_denoise(ctypes.byref(fp8), None) == 3
 
 
 def test_batched_workspace_sizes(lib):

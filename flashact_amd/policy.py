@@ -7,6 +7,8 @@ front-end (vision encoder, tokenizer, encoder CUDA graph), which is outside this
     ``time_mlp_in/out``, ``action_in/out_proj``; hybrid_model.py:94-132), read from a
     ``.safetensors`` file or a state dict; the backbone layers (for the prefill) from the PaliGemma
     language-model keys of the same checkpoint;
+  * ``weight_format="fp8"`` quantises the expert weights per row to e4m3 as the reference does
+    (hybrid_model.py:105-110) and runs the FP8-W8A16 loop;
   * the adaRMS modulations are computed once on the device for the fixed schedule
     t_i = 1 - i / num_steps (hybrid_model.py:111-128);
   * ``predict`` takes the prefix either as hidden states (the backbone prefill runs on the GPU and
@@ -74,7 +76,11 @@ class Pi05Policy:
     """Expert (and optionally backbone) weights resident on one GPU, ready for ``predict``."""
 
     def __init__(self, checkpoint, *, num_steps: int = 10, chunk_size: int = 50, device="cuda",
-                 initial_noise_mode: str = "gaussian", initial_noise_scale: float = 1.0, load_backbone: bool = True):
+                 initial_noise_mode: str = "gaussian", initial_noise_scale: float = 1.0, load_backbone: bool = True,
+                 weight_format: str = "bf16"):
+        if weight_format not in {"bf16", "fp8"}:
+            raise ValueError(f"weight_format must be 'bf16' or 'fp8' (per-row e4m3, as the reference), got {weight_format}")
+        self.weight_format = weight_format
         if initial_noise_mode not in {"gaussian", "zero", "scale"}:
             raise ValueError(f"unsupported initial noise mode: {initial_noise_mode}")
         if not 1 <= chunk_size <= 64:
@@ -100,10 +106,10 @@ class Pi05Policy:
     def _load_expert(self, src):
         NL, dev = self.num_layers, self.device
         st = lambda n: self._stack(src, EXPERT, n, NL)  # noqa: E731
-        self.packed = pi05.pack_weights(st("self_attn.q_proj.weight"), st("self_attn.k_proj.weight"),
-                                        st("self_attn.v_proj.weight"), st("self_attn.o_proj.weight"),
-                                        st("mlp.gate_proj.weight"), st("mlp.up_proj.weight"),
-                                        st("mlp.down_proj.weight"))
+        pack = pi05.pack_weights_fp8 if self.weight_format == "fp8" else pi05.pack_weights
+        self.packed = pack(st("self_attn.q_proj.weight"), st("self_attn.k_proj.weight"),
+                           st("self_attn.v_proj.weight"), st("self_attn.o_proj.weight"),
+                           st("mlp.gate_proj.weight"), st("mlp.up_proj.weight"), st("mlp.down_proj.weight"))
         f = lambda k: src[k].float().to(dev).contiguous()  # noqa: E731
         self.mods, self.mod_final = pi05.precompute_mods(
             self.num_steps, f("time_mlp_in.weight"), f("time_mlp_in.bias"), f("time_mlp_out.weight"),
@@ -170,7 +176,8 @@ class Pi05Policy:
         cos, sin = pi05.rope_table(Lp, self.chunk_size, device=dev)
         p = self.packed
         empty = torch.empty(0, device=dev)
-        pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], empty, empty, empty, empty, self.mods, self.mod_final,
+        sc = [p.get(k, empty) for k in ("s1", "so", "s2", "s3")]
+        pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], *sc, self.mods, self.mod_final,
                     cos, sin, self.w_ain, self.b_ain, self.w_aout, self.b_aout, ksrc, vsrc, srows, kc, vc, Lp, Lmax,
                     self.num_steps, self.chunk_size, x_t)
         return x_t.cpu().numpy()

@@ -73,12 +73,14 @@ typedef struct fa_device_info {
  * and updates x_t in place: x_t [batch][xt_rows][32] fp32, rows [0, Tv) of each sample.
  */
 typedef struct fa_pi05_args {
-  int weight_dtype; /* FA_DTYPE_BF16 (FA_DTYPE_FP8_E4M3 reserved) */
+  int weight_dtype; /* FA_DTYPE_BF16, or FA_DTYPE_FP8_E4M3 (batch 1): e4m3 codes in the same packed
+                     * layouts with one fp32 scale per packed row in s1 [NL][2560], so [NL][1024],
+                     * s2 [NL][8192], s3 [NL][1024] (src/pi05/hybrid_model.py:105-110) */
   const void* w1;
   const void* wo;
   const void* w2;
   const void* w3;
-  const float* s1; /* per-row fp8 scales; must be NULL for bf16 weights */
+  const float* s1; /* per-row fp8 scales (16-byte aligned); must be NULL for bf16 weights */
   const float* so;
   const float* s2;
   const float* s3;

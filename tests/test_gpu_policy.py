@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 NL, LP, T, S = 2, 200, 50, 2
 
 
-def _oracle_chain(sd, pol, x, noise, K=None, V=None):
+def _oracle_chain(sd, pol, x, noise, K=None, V=None, fp8=False):
     from oracle import oracle as O
     E, B = PC.EXPERT, PC.BACKBONE
     st = lambda p, n: torch.stack([sd[f"{p}layers.{i}.{n}"] for i in range(NL)]).cpu()  # noqa: E731
@@ -40,6 +40,12 @@ def _oracle_chain(sd, pol, x, noise, K=None, V=None):
               rope_sin=sin.numpy(), w_ain=f("action_in_proj.weight"), b_ain=f("action_in_proj.bias"),
               w_aout=f("action_out_proj.weight"), b_aout=f("action_out_proj.bias"),
               kpre=P.u16(K.reshape(1, NL, LP, 256)), vpre=P.u16(V.reshape(1, NL, LP, 256)))
+    if fp8:  # the expert's per-row e4m3 codes and scales, natural layouts
+        for n, m in (("q", "self_attn.q_proj"), ("k", "self_attn.k_proj"), ("v", "self_attn.v_proj"),
+                     ("o", "self_attn.o_proj"), ("g", "mlp.gate_proj"), ("u", "mlp.up_proj"), ("d", "mlp.down_proj")):
+            q, sc = pi05.quantize_fp8(st(E, f"{m}.weight"))
+            ew["q" + n], ew["s" + n] = q.numpy(), sc.numpy()
+        return O.pi05_denoise_fp8(ew, noise.cpu().numpy()[None], Lp=LP, Tv=T, S=S, NL=NL)[0]
     return O.pi05_denoise(ew, noise.cpu().numpy()[None], Lp=LP, Tv=T, S=S, NL=NL)[0]
 
 
@@ -92,3 +98,17 @@ def test_noise_modes(setup):
     g1 = torch.Generator(device=x.device).manual_seed(9)
     g2 = torch.Generator(device=x.device).manual_seed(9)
     assert torch.allclose(sc.initial_noise(g1), 0.5 * pol.initial_noise(g2))
+
+
+def test_predict_fp8_weights(setup):
+    """weight_format="fp8": the expert runs FP8-W8A16 on the per-row e4m3 codes of the same checkpoint,
+    against the oracle chain with the oracle's fp8 loop on those codes."""
+    sd, pol, x, noise = setup
+    pol8 = policy.Pi05Policy(sd, num_steps=S, chunk_size=T, device=x.device, weight_format="fp8")
+    assert pol8.packed["w1"].dtype == torch.uint8 and "s1" in pol8.packed
+    out = pol8.predict(x, noise=noise)
+    ref = _oracle_chain(sd, pol8, x, noise, fp8=True)
+    st = P.parity(out, ref)
+    print(f"policy fp8 path: {st}", flush=True)
+    assert st["max_abs"] <= 2e-2 and st["mean_abs"] <= 2e-3, st
+    assert not np.array_equal(out, pol.predict(x, noise=noise))  # the weights really are quantised

@@ -63,7 +63,8 @@ constexpr uint32_t L_RED = 36 * 1024;               // cross-wave reduction [4 w
 constexpr uint32_t L_X = L_RED + 16 * 1024;         // residual x of token r [768] f32
 constexpr uint32_t L_XT = L_X + D * 4;              // x_t of token r [32] f32
 constexpr uint32_t L_MISC = L_XT + AD * 4;          // [4 waves][768] f32 exchange partial sums
-constexpr uint32_t LDS_BYTES = L_MISC + 4 * D * 4;
+constexpr uint32_t L_ROPE = L_MISC + 4 * D * 4;     // rank 0: RoPE cos | sin [2][32 tokens][48] f32
+constexpr uint32_t LDS_BYTES = L_ROPE + 2 * TP * 48 * 4;
 
 struct Params {
   const bf16 *w_qkv, *w_so, *w_cq, *w_co, *w_gu, *w_dn;
@@ -356,7 +357,8 @@ __device__ __forceinline__ void stage_satt(const Params& p, const Ctx& c) {
 #pragma unroll
   for (int i = 0; i < 24; i++) {
     const float qo = __shfl_xor(q[i], 32, 64), ko = __shfl_xor(k[i], 32, 64);
-    const float cs = p.rope_cos[(tv ? tau : 0) * 48 + j0 + i], sn = p.rope_sin[(tv ? tau : 0) * 48 + j0 + i];
+    const float* rope = reinterpret_cast<const float*>(lds + L_ROPE);  // staged by the prologue
+    const float cs = rope[(tv ? tau : 0) * 48 + j0 + i], sn = rope[TP * 48 + (tv ? tau : 0) * 48 + j0 + i];
     q[i] = lo ? q[i] * cs - qo * sn : qo * sn + q[i] * cs;
     k[i] = lo ? k[i] * cs - ko * sn : ko * sn + k[i] * cs;
   }
@@ -587,6 +589,13 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
   }
   float* xt = reinterpret_cast<float*>(lds + L_XT);
   if (c.w == 0 && c.lane < AD && c.r < p.Tv) xt[c.lane] = p.x_t[c.r * AD + c.lane];
+  if (c.r == 0) {  // the RoPE table of the self-attention rank, read every layer
+    float* rope = reinterpret_cast<float*>(lds + L_ROPE);
+    for (int i = threadIdx.x; i < p.Tv * 48; i += NTHR) {
+      rope[i] = p.rope_cos[i];
+      rope[TP * 48 + i] = p.rope_sin[i];
+    }
+  }
   __syncthreads();
   // exchange e uses buffer e & 1; the n-th use of a buffer carries parity (1 + base + n) & 1
   auto buf = [](int e) { return e & 1; };

@@ -112,15 +112,60 @@ __device__ __forceinline__ float bf_hi(unsigned u) { return __builtin_bit_cast(f
 
 __device__ __forceinline__ unsigned xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 7u; }
 
+// Cross-lane reductions without LDS round trips (lane layouts checked on gfx950 hardware):
+//  * DPP inside a 16-lane row: quad_perm [1,0,3,2] (lane ^ 1), [2,3,0,1] (lane ^ 2),
+//    row_half_mirror (i -> 7 - i in each half row), row_mirror (i -> 15 - i);
+//  * v_permlane16_swap(x, y): lanes of even rows get {x own, x of lane + 16}, odd rows
+//    {y of lane - 16, y own}, i.e. result[0] comes from the lower lane, result[1] from the upper;
+//  * v_permlane32_swap: the same between the two 32-lane halves.
+// Each combine applies the operator as (lower lane, upper lane), so every lane of a reduction
+// group ends with the bit-identical value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return as_f32((unsigned)__builtin_amdgcn_update_dpp(0, (int)as_u32(v), CTRL, 0xF, 0xF, false));
+}
+struct LanePair {
+  unsigned lo, hi;
+};
+__device__ __forceinline__ LanePair swap16(unsigned x, unsigned y) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+  return {r[0], r[1]};
+}
+__device__ __forceinline__ LanePair swap32(unsigned x, unsigned y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+  return {r[0], r[1]};
+}
+// Sum / max over the lanes {l, l ^ 16, l ^ 32, l ^ 48} (the four row-quarters of a column).
+__device__ __forceinline__ float cols_sum(float v) {
+  LanePair a = swap16(as_u32(v), as_u32(v));
+  v = as_f32(a.lo) + as_f32(a.hi);
+  a = swap32(as_u32(v), as_u32(v));
+  return as_f32(a.lo) + as_f32(a.hi);
+}
+__device__ __forceinline__ float cols_max(float v) {
+  LanePair a = swap16(as_u32(v), as_u32(v));
+  v = fmaxf(as_f32(a.lo), as_f32(a.hi));
+  a = swap32(as_u32(v), as_u32(v));
+  return fmaxf(as_f32(a.lo), as_f32(a.hi));
+}
+// Value of lane ^ 16 (selected from the swap of x with itself).
+__device__ __forceinline__ unsigned xor16_u32(unsigned x, bool odd_row) {
+  const LanePair a = swap16(x, x);
+  return odd_row ? a.lo : a.hi;
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v = dpp_f32<0xB1>(v) + v;
+  v = dpp_f32<0x4E>(v) + v;
+  v = dpp_f32<0x141>(v) + v;
+  v = dpp_f32<0x140>(v) + v;
+  return cols_sum(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(dpp_f32<0xB1>(v), v);
+  v = fmaxf(dpp_f32<0x4E>(v), v);
+  v = fmaxf(dpp_f32<0x141>(v), v);
+  v = fmaxf(dpp_f32<0x140>(v), v);
+  return cols_max(v);
 }
 
 __device__ __forceinline__ float gelu_tanh(float x) {

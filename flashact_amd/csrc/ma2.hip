@@ -356,7 +356,8 @@ __device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, const YSr
     const int j0 = 24 * (g4 & 1);
 #pragma unroll
     for (int i = 0; i < 24; i++) {
-      const float qo = __shfl_xor(q[i], 32, 64), ko = __shfl_xor(k[i], 32, 64);
+      const LanePair sq = swap32(as_u32(q[i]), as_u32(q[i])), sk = swap32(as_u32(k[i]), as_u32(k[i]));
+      const float qo = as_f32(lo ? sq.hi : sq.lo), ko = as_f32(lo ? sk.hi : sk.lo);  // lane ^ 32
       const float c = p.rope_cos[(tv ? tau : 0) * 48 + j0 + i], sn = p.rope_sin[(tv ? tau : 0) * 48 + j0 + i];
       q[i] = lo ? q[i] * c - qo * sn : qo * sn + q[i] * c;
       k[i] = lo ? k[i] * c - ko * sn : ko * sn + k[i] * c;

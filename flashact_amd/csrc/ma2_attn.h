@@ -46,8 +46,7 @@ __device__ __forceinline__ void attend(const u32x4 (&qf)[3], uint32_t kbase, uin
       s[kt][i] = key < kvalid ? s[kt][i] * qscale : -1e30f;
       m_ = fmaxf(m_, s[kt][i]);
     }
-  m_ = fmaxf(m_, __shfl_xor(m_, 16, 64));
-  m_ = fmaxf(m_, __shfl_xor(m_, 32, 64));
+  m_ = cols_max(m_);
   float ps = 0.f;
   u32x4 pb[NKT / 2];
 #pragma unroll
@@ -63,8 +62,7 @@ __device__ __forceinline__ void attend(const u32x4 (&qf)[3], uint32_t kbase, uin
     pb[sp] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
                    pack_bf16x2(pv[6], pv[7])};
   }
-  ps += __shfl_xor(ps, 16, 64);
-  ps += __shfl_xor(ps, 32, 64);
+  ps = cols_sum(ps);
   const float inv = 1.0f / ps;
 #pragma unroll
   for (int dt = 0; dt < 6; dt++) {
@@ -87,8 +85,7 @@ __device__ __forceinline__ void rms96(float (&v)[24]) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 24; i++) ss += v[i] * v[i];
-  ss += __shfl_xor(ss, 16, 64);
-  ss += __shfl_xor(ss, 32, 64);
+  ss = cols_sum(ss);
   const float r = rsqrtf(ss / (float)HD + 1e-6f);
 #pragma unroll
   for (int i = 0; i < 24; i++) v[i] *= r;

@@ -356,7 +356,8 @@ __device__ __forceinline__ void stage_satt(const Params& p, const Ctx& c) {
   const int j0 = 24 * (g4 & 1);
 #pragma unroll
   for (int i = 0; i < 24; i++) {
-    const float qo = __shfl_xor(q[i], 32, 64), ko = __shfl_xor(k[i], 32, 64);
+    const LanePair sq = swap32(as_u32(q[i]), as_u32(q[i])), sk = swap32(as_u32(k[i]), as_u32(k[i]));
+      const float qo = as_f32(lo ? sq.hi : sq.lo), ko = as_f32(lo ? sk.hi : sk.lo);  // lane ^ 32
     const float* rope = reinterpret_cast<const float*>(lds + L_ROPE);  // staged by the prologue
     const float cs = rope[(tv ? tau : 0) * 48 + j0 + i], sn = rope[TP * 48 + (tv ? tau : 0) * 48 + j0 + i];
     q[i] = lo ? q[i] * cs - qo * sn : qo * sn + q[i] * cs;
@@ -444,8 +445,7 @@ __device__ __forceinline__ void stage_catt(const Params& p, const Ctx& c, const 
       s[kt][i] = key < p.Lk ? s[kt][i] * qscale : -1e30f;
       m_ = fmaxf(m_, s[kt][i]);
     }
-  m_ = fmaxf(m_, __shfl_xor(m_, 16, 64));
-  m_ = fmaxf(m_, __shfl_xor(m_, 32, 64));
+  m_ = cols_max(m_);
   float pv[8], ps = 0.f;
 #pragma unroll
   for (int kt = 0; kt < 2; kt++)
@@ -454,8 +454,7 @@ __device__ __forceinline__ void stage_catt(const Params& p, const Ctx& c, const 
       pv[4 * kt + i] = exp2f(s[kt][i] - m_);
       ps += pv[4 * kt + i];
     }
-  ps += __shfl_xor(ps, 16, 64);
-  ps += __shfl_xor(ps, 32, 64);
+  ps = cols_sum(ps);
   const u32x4 pb = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
                     pack_bf16x2(pv[6], pv[7])};
   const int nv = min(max(p.Lk - (key0 + 8 * c.lq), 0), 8);

@@ -158,8 +158,7 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
             s[q][kt8][i] = key < kend ? s[q][kt8][i] * qscale : -1e30f;
             m_ = fmaxf(m_, s[q][kt8][i]);
           }
-        m_ = fmaxf(m_, __shfl_xor(m_, 16, 64));
-        m_ = fmaxf(m_, __shfl_xor(m_, 32, 64));
+        m_ = cols_max(m_);
         float ps = 0.f;
 #pragma unroll
         for (int sp = 0; sp < 4; sp++) {
@@ -174,8 +173,7 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
           pb[q][sp] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
                             pack_bf16x2(pv[6], pv[7])};
         }
-        ps += __shfl_xor(ps, 16, 64);
-        ps += __shfl_xor(ps, 32, 64);
+        ps = cols_sum(ps);
         mx[q] = m_;
         psum[q] = ps;
       }

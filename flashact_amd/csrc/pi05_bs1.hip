@@ -138,6 +138,11 @@ __device__ __forceinline__ void stamp(const Ctx& c, int i) {
   if (c.tr && c.lane == 0) c.tr[i] = __builtin_amdgcn_s_memrealtime();
 }
 
+// Lane indices pass through an empty asm at every stage boundary, so the compiler recomputes the
+// addresses derived from them inside each stage instead of keeping them live across the whole
+// layer (which pushes the kernel past 256 VGPRs into scratch spills on the hot path).
+__device__ __forceinline__ void launder(Ctx& c) { asm volatile("" : "+v"(c.lane), "+v"(c.lr), "+v"(c.lq)); }
+
 // LDS control words (ready[2], consumed[4], abort) shared by the loader and compute waves of a
 // workgroup: relaxed workgroup-scope atomics, which compile to plain ds_read/ds_write (a volatile
 // access would keep the generic address space and become a flat access).
@@ -751,8 +756,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
         s[kt][i] = key < kend ? s[kt][i] * qscale : -1e30f;
         bmax = fmaxf(bmax, s[kt][i]);
       }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    bmax = cols_max(bmax);
     const float mnew = fmaxf(m, bmax);
     const float alpha = exp2f(m - mnew);
     m = mnew;
@@ -769,8 +773,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
       pk[kt * 2 + 0] = pack_bf16x2(pv[0], pv[1]);
       pk[kt * 2 + 1] = pack_bf16x2(pv[2], pv[3]);
     }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
+    psum = cols_sum(psum);
     lsum = lsum * alpha + psum;
     // B operand P^T: k-slot 8lq+i <-> key kg0+i (i<4), kg0+16+(i-4) (i>=4); V^T uses the same order
     const u32x4 pb = {pk[0], pk[1], pk[2], pk[3]};
@@ -934,7 +937,8 @@ __device__ __forceinline__ void stage_gu(const Params& p, const Ctx& c, int l, i
   const unsigned p0 = pack_bf16x2(gelu_tanh(acc[0][0]) * acc[0][1], gelu_tanh(acc[0][2]) * acc[0][3]);
   const unsigned p1 = pack_bf16x2(gelu_tanh(acc[1][0]) * acc[1][1], gelu_tanh(acc[1][2]) * acc[1][3]);
   const bool odd = c.lq & 1;
-  const unsigned recv = (unsigned)__shfl_xor((int)(odd ? p0 : p1), 16, 64);
+  const LanePair sw = swap16(p0, p1);  // even rows receive the odd partner's p0, odd rows the even partner's p1
+  const unsigned recv = odd ? sw.lo : sw.hi;
   const u32x2 out = odd ? u32x2{recv, p1} : u32x2{p0, recv};
   const int f0 = odd ? 8 + 2 * (c.lq - 1) : 2 * c.lq;
   *reinterpret_cast<u32x2*>(p.ws + OFF_H + c.g * (TP * 512 * 2) + frag_off(16, t, 16 * c.r + f0)) = out;
@@ -1035,9 +1039,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
   for (int step = 0; step < p.S; step++) {
 #pragma unroll 1
     for (int l = 0; l < NL; l++) {
-      // Lane indices are laundered each layer so the compiler recomputes addresses inside the
-      // loop instead of hoisting hundreds of loop-invariant offsets (which spill).
-      asm volatile("" : "+v"(c.lane), "+v"(c.lr), "+v"(c.lq));
+      launder(c);
       const int li = step * NL + l;
       const int pb = li * PG::PPL;
       const unsigned par = (1u + xbase + (unsigned)li) & 1u;
@@ -1054,24 +1056,28 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       stamp(c, 1);
       mark(p, c, 0, t0);
       xcd_sync(p, c);
+      launder(c);
       mark(p, c, 9, t0);
       stamp(c, 2);
       stage_qkv<FP8>(p, c, l, pb + PG::QKV, step == p.S - 1);
       stamp(c, 3);
       mark(p, c, 1, t0);
       xcd_sync(p, c);
+      launder(c);
       mark(p, c, 9, t0);
       stamp(c, 4);
       stage_att(p, c, l, pb + PG::K);
       stamp(c, 5);
       mark(p, c, 2, t0);
       xcd_sync(p, c);
+      launder(c);
       mark(p, c, 9, t0);
       stamp(c, 6);
       stage_comb(p, c);
       stamp(c, 7);
       mark(p, c, 3, t0);
       xcd_sync(p, c);
+      launder(c);
       mark(p, c, 9, t0);
       stamp(c, 8);
       stage_oproj<FP8>(p, c, l, pb + PG::O, par);
@@ -1081,12 +1087,14 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       stamp(c, 10);
       mark(p, c, 5, t0);
       xcd_sync(p, c);
+      launder(c);
       mark(p, c, 9, t0);
       stamp(c, 11);
       stage_gu<FP8>(p, c, l, pb + PG::GU);
       stamp(c, 12);
       mark(p, c, 6, t0);
       xcd_sync(p, c);
+      launder(c);
       mark(p, c, 9, t0);
       stamp(c, 13);
       stage_dn<FP8>(p, c, l, pb + PG::DN, par);

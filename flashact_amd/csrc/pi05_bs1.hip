@@ -66,7 +66,7 @@ constexpr uint32_t OFF_XFLAG = 1024; // [8 XCD][32 rank][4 wave] u64 epochs
 // wave loads as the B operand is contiguous (see frag_off).
 constexpr uint32_t OFF_XN = kWsDataBase;                                  // [8][4][32][16][4][8] bf16
 constexpr uint32_t OFF_Q = OFF_XN + NX * TP * D * 2;                // [8][4][8][16][4][8] bf16
-constexpr uint32_t OFF_ATTP = OFF_Q + NX * TP * HD * 2;             // [8][32][64][256] bf16
+constexpr uint32_t OFF_ATTP = OFF_Q + NX * TP * HD * 2;             // [8][32 chunks][4][8][16][4][8] bf16
 constexpr uint32_t OFF_ATTML = OFF_ATTP + NX * NCH * TP * HD * 2;   // [8][32][64][2] f32
 constexpr uint32_t OFF_ATTN = OFF_ATTML + NX * NCH * TP * 2 * 4;    // [8][4][8][16][4][8] bf16
 constexpr uint32_t OFF_H = OFF_ATTN + NX * TP * HD * 2;             // [8][4][16][16][4][8] bf16
@@ -82,10 +82,12 @@ constexpr uint32_t WS_BYTES = OFF_VFR + NX * NSB * 16384;
 static_assert(OFF_XFLAG + NX * NR * NCW * 8 <= kWsCounters, "flags stay below the fixup counters");
 
 // LDS layout (bytes)
-constexpr uint32_t L_CTL = RING * PAGE;        // u32 ready[2], consumed[4], abort
+constexpr uint32_t L_CTL = RING * PAGE;        // u32 ready[2], consumed[4], abort, -, staging count, combine count
 constexpr uint32_t L_XRES = L_CTL + 64;        // f32 [2][1024] residual stream of tokens r, r+32
 constexpr uint32_t L_XT = L_XRES + 2 * D * 4;  // f32 [2][32] x_t of tokens r, r+32
-constexpr uint32_t LDS_BYTES = L_XT + 2 * AD * 4;
+constexpr uint32_t L_COMB = L_XT + 2 * AD * 4;  // f32 [3][64][10] combine hand-off (waves 1-3 -> 0)
+constexpr uint32_t LDS_BYTES = L_COMB + 3 * 64 * 10 * 4;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS of one CU");
 
 // Byte offset of element (token t, k) of a fragment-ordered operand with KS k-steps of 32,
 // relative to the XCD's block (XCD block size = 64 * 32 * KS * 2 bytes).
@@ -415,22 +417,32 @@ __device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0
       for (int k = 0; k < KC; k++) xf[(ck + 1) & 1][k] = ldb128<kCpSc1>(c.ws, xoff + ((ck + 1) * KC + k) * XSTRIDE);
     }
     __builtin_amdgcn_sched_barrier(0);
+    // A fragments are read from LDS in batches of AB ahead of their MFMAs (left to itself the
+    // compiler keeps about two reads in flight and every MFMA waits out an LDS round trip)
+    constexpr int NA = KC * RT, AB = NA < 8 ? NA : 8;
 #pragma unroll
-    for (int k = 0; k < KC; k++)
+    for (int h = 0; h < NA; h += AB) {
+      u32x4 af[AB];
 #pragma unroll
-      for (int rt = 0; rt < RT; rt++) {
-        u32x4 a;
+      for (int j = 0; j < AB; j++) {
+        const int k = (h + j) / RT, rt = (h + j) % RT;
         if constexpr (FP8) {
           const int ks = ck * KC + k, P = rt * PRT + (ks >> 1);
           const u32x2 q = *reinterpret_cast<const u32x2*>(fa_lds + slot[P >> 4] + (P & 15) * 1024 + 512 * (ks & 1));
-          a = fp8x8_to_bf16(q[0], q[1]);
+          af[j] = fp8x8_to_bf16(q[0], q[1]);
         } else {
           const int F = rt * KS + ck * KC + k;
-          a = *reinterpret_cast<const u32x4*>(fa_lds + slot[F >> 4] + (F & 15) * 1024);
+          af[j] = *reinterpret_cast<const u32x4*>(fa_lds + slot[F >> 4] + (F & 15) * 1024);
         }
-        ac2[rt][k & 1] = mfma16(a, xf[ck & 1][k], ac2[rt][k & 1]);
       }
-    __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < AB; j++) {
+        const int k = (h + j) / RT, rt = (h + j) % RT;
+        ac2[rt][k & 1] = mfma16(af[j], xf[ck & 1][k], ac2[rt][k & 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 #pragma unroll
   for (int rt = 0; rt < RT; rt++) acc[rt] = ac2[rt][0] + ac2[rt][1];
@@ -632,12 +644,13 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
     if (vr0 >= 512) {
       if (!tv) continue;
       const int d = vr0 - 512;
-      // value dims d..d+3 of key Lp+t into the fragment-ordered copy (lane dim%16 + 16*(key%16/4))
+      // value dims d..d+3 of key Lp+t into the XCD's copy of its 32-key block, laid out as the V^T
+      // ring page: dim tile d/16, lane d%16 + 16 (j/8), element j%8 for key offset j
       const int kp = p.Lp + t, st = (kp >> 5) - (p.Lp >> 5), j = kp & 31;
-      bf16* vf = reinterpret_cast<bf16*>(p.ws + OFF_VFR) +
-                 ((((c.g * NSB + st) * 16 + (d >> 4)) * 2 + (j >> 4)) * 64 + 16 * ((j & 15) >> 2)) * 4 + (j & 3);
+      bf16* vf = reinterpret_cast<bf16*>(p.ws + OFF_VFR + (c.g * NSB + st) * 16384) +
+                 ((d >> 4) * 64 + (d & 15) + 16 * (j >> 3)) * 8 + (j & 7);
 #pragma unroll
-      for (int i = 0; i < 4; i++) vf[((d & 15) + i) * 4] = (bf16)v[i];
+      for (int i = 0; i < 4; i++) vf[i * 8] = (bf16)v[i];
       if (last && c.g == (l & 7)) {
         bf16* vr = p.vtcache + ((size_t)l * HD + d) * p.Lmax + p.Lp + t;
 #pragma unroll
@@ -675,17 +688,69 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
 }
 
 // ---------------------------------------------------------------- attention partials
+// This step's keys inside a rank's first 32-key block go from the XCD's suffix copies (written by
+// QKV) into the K and V^T ring pages, over the rows the loader brought from the caches, so the
+// whole block is then read from LDS. The four compute waves share the copy (4 fragments of each
+// page per wave, one L2 round trip) and meet on an LDS counter that reaches `target`. A V^T lane
+// slot holds 8 keys; one that straddles Lp keeps its prefix elements from the page.
+__device__ __forceinline__ void stage_suffix(const Params& p, const Ctx& c, int kb, int pgk, unsigned target) {
+  const int st = (kb >> 5) - (p.Lp >> 5);
+  const uint32_t kslot = (pgk % RING) * PAGE, vslot = ((pgk + 1) % RING) * PAGE;
+  const uint32_t kfr = OFF_KFR + (c.g * NSB + st) * 16384, vfr = OFF_VFR + (c.g * NSB + st) * 16384;
+  const bool ksfx = kb + 16 * (c.wave >> 1) + c.lr >= p.Lp;  // key row of this lane in fragments 4w..4w+3
+  const int npre = min(max(p.Lp - (kb + 8 * c.lq), 0), 8);    // prefix keys of this lane's V^T slot
+  u32x4 kv[4], vv[4], pv[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t f = 4 * c.wave + i;
+    kv[i] = ldb128<kCpSc1>(c.ws, ksfx ? kfr + f * 1024 + c.lane * 16 : OOB);
+    vv[i] = ldb128<kCpSc1>(c.ws, npre < 8 ? vfr + f * 1024 + c.lane * 16 : OOB);
+    pv[i] = *reinterpret_cast<const u32x4*>(fa_lds + vslot + f * 1024 + c.lane * 16);
+  }
+  unsigned keep[4];  // page elements kept: element e of the slot is key kb + 8 lq + e
+#pragma unroll
+  for (int m = 0; m < 4; m++) keep[m] = (2 * m < npre ? 0xffffu : 0u) | (2 * m + 1 < npre ? 0xffff0000u : 0u);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t f = 4 * c.wave + i;
+    if (ksfx) *reinterpret_cast<u32x4*>(fa_lds + kslot + f * 1024 + c.lane * 16) = kv[i];
+    if (npre < 8) {
+      u32x4 o;
+#pragma unroll
+      for (int m = 0; m < 4; m++) o[m] = (pv[i][m] & keep[m]) | (vv[i][m] & ~keep[m]);
+      *reinterpret_cast<u32x4*>(fa_lds + vslot + f * 1024 + c.lane * 16) = o;
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's page writes are done
+  unsigned* cnt = reinterpret_cast<unsigned*>(fa_lds + L_CTL) + 8;
+  if (c.lane == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  for (unsigned it = 0;; ++it) {
+    if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target || ctl_ld(6)) break;
+    if (it > kSpinCap) {
+      ctl_st(6, 1u);
+      if (c.lane == 0) atomicOr(c.err, kErrSpin);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");  // page reads stay after the meeting
+}
+
 // Head g, keys [kbeg, kend) of chunk r (C = 32 ceil(Ltot/1024) keys), tokens of this wave's tile,
 // in 32-key blocks. Sources per key (K rows) or 4-key group (V^T columns): prefix keys of the
 // first block come from the LDS pages the loader prefetched, prefix keys of later blocks from the
 // caches, this step's keys from the XCD-private fragment-ordered copies; a 4-key group that
 // straddles Lp takes its prefix and suffix elements from both. Keys past kend: S = -inf, V = 0.
-__device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, int pgk) {
+__device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, int pgk, int li) {
   const int Ltot = p.Lp + p.Tv;
   const int C = 32 * ((Ltot + 32 * NCH - 1) / (32 * NCH));
   const int kbeg = c.kb0, kend = min(kbeg + C, Ltot);
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
+  if (kbeg < kend && min(kbeg + 32, kend) > p.Lp) {  // the first block holds keys of this step
+    page_wait(c, pgk + 1);
+    stage_suffix(p, c, kbeg, pgk, 4u * (unsigned)(li + 1));
+  }
   if (16 * c.wave >= p.Tv) {
     page_release(c, pgk + 2);
     return;
@@ -706,7 +771,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) qf[ks] = ldb128<kCpSc1>(c.ws, qb + ks * 1024);
   }
-  if (kbeg < p.Lp) page_wait(c, pgk + 1);
+  page_wait(c, pgk + 1);
   stamp(c, 23);
   const uint32_t kslot = (pgk % RING) * PAGE, vslot = ((pgk + 1) % RING) * PAGE;
 
@@ -727,14 +792,14 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
     for (int kt = 0; kt < 2; kt++) {
       u32x4 kf[8];
       const int key = kb + kt * 16 + c.lr;
-      if (key >= p.Lp) {
-        const uint32_t rb = key < kend ? OFF_KFR + (((c.g * NSB + st) * 2 + kt) * 8) * 1024 + c.lane * 16 : OOB;
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) kf[ks] = ldb128<kCpSc1>(c.ws, rb + ks * 1024);
-      } else if (first) {
+      if (first) {  // the ring page (this step's keys staged into it)
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
           kf[ks] = *reinterpret_cast<const u32x4*>(fa_lds + kslot + (kt * 8 + ks) * 1024 + c.lane * 16);
+      } else if (key >= p.Lp) {
+        const uint32_t rb = key < kend ? OFF_KFR + (((c.g * NSB + st) * 2 + kt) * 8) * 1024 + c.lane * 16 : OOB;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) kf[ks] = ldb128<kCpSc1>(c.ws, rb + ks * 1024);
       } else {
         const uint32_t rb = kl + key * HD * 2 + c.lq * 16;
 #pragma unroll
@@ -794,22 +859,22 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
 #pragma unroll
       for (int h2 = 0; h2 < 2; h2++) {
         const int kg = kg0 + 16 * h2;
-        if (npre[h2] > 0) {  // prefix elements: LDS page (first block) or the cache
-          if (first) {
-            const int o8 = 16 * h2 + 4 * c.lq;  // key offset within the 32-key block
-            const uint32_t ad = vslot + (c.lr + 16 * (o8 >> 3)) * 16 + (o8 & 7) * 2 + half * 8 * 1024;
+        if (first) {  // the ring page (this step's keys staged into it)
+          const int o8 = 16 * h2 + 4 * c.lq;  // key offset within the 32-key block
+          const uint32_t ad = vslot + (c.lr + 16 * (o8 >> 3)) * 16 + (o8 & 7) * 2 + half * 8 * 1024;
 #pragma unroll
-            for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = *reinterpret_cast<const u32x2*>(fa_lds + ad + d8 * 1024);
-          } else {
-            const uint32_t vo = vl + c.lr * p.Lmax * 2 + kg * 2 + half * 8 * vstep;
-#pragma unroll
-            for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = ldb64<kCpPlain>(c.vc, vo + d8 * vstep);
-          }
+          for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = *reinterpret_cast<const u32x2*>(fa_lds + ad + d8 * 1024);
+          continue;
         }
-        if (npre[h2] < 4) {  // this step's elements from the fragment-ordered copy
-          const uint32_t vo = kg < kend
-                                  ? OFF_VFR + ((((c.g * NSB + st) * 16 + half * 8) * 2 + h2) * 64 + c.lane) * 8
-                                  : OOB;
+        if (npre[h2] > 0) {  // prefix elements from the cache
+          const uint32_t vo = vl + c.lr * p.Lmax * 2 + kg * 2 + half * 8 * vstep;
+#pragma unroll
+          for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = ldb64<kCpPlain>(c.vc, vo + d8 * vstep);
+        }
+        if (npre[h2] < 4) {  // this step's elements from the XCD's copy (V^T page layout)
+          const uint32_t vo = kg < kend ? OFF_VFR + (c.g * NSB + st) * 16384 +
+                                              (half * 8 * 64 + c.lr + 16 * (2 * h2 + (c.lq >> 1))) * 16 + 8 * (c.lq & 1)
+                                        : OOB;
           if (npre[h2] == 0) {
 #pragma unroll
             for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = ldb64<kCpSc1>(c.ws, vo + d8 * 1024);
@@ -836,50 +901,108 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
   }
   stamp(c, 24);
   page_release(c, pgk + 2);
-  // lane holds O^T[dim 16dt + 4lq + i][token lr]: store O / l (bf16) and (m, l)
-  if (tv) {
+  // O^T / l (bf16) in the O projection's operand order: fragment ks of this token tile holds dims
+  // 32ks..32ks+31, slot (token, q) dims 32ks + 8q..+7. A lane holds dims 16dt + 4lq + i of token lr,
+  // so slot q = lq/2 + 2 (lq%2) of tiles (2ks, 2ks+1) is completed by the lane ^ 16 partner's four
+  // dims (one swap per dword), and every store writes one whole 1 KB fragment.
+  {
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
-    const uint32_t base = OFF_ATTP + (pbase * HD + c.lq * 4) * 2;
+    const bool odd = c.lq & 1;
+    const uint32_t ob = OFF_ATTP + ((c.g * NCH + c.r) * (TP / 16) + c.wave) * 8192 +
+                        (c.lr * 4 + (c.lq >> 1) + 2 * (c.lq & 1)) * 16;
 #pragma unroll
-    for (int dt = 0; dt < 16; dt++) {
-      const u32x2 pk = {pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv), pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv)};
-      *reinterpret_cast<u32x2*>(p.ws + base + dt * 32) = pk;
+    for (int ks = 0; ks < 8; ks++) {
+      const unsigned a0 = pack_bf16x2(o[2 * ks][0] * inv, o[2 * ks][1] * inv);
+      const unsigned a1 = pack_bf16x2(o[2 * ks][2] * inv, o[2 * ks][3] * inv);
+      const unsigned b0 = pack_bf16x2(o[2 * ks + 1][0] * inv, o[2 * ks + 1][1] * inv);
+      const unsigned b1 = pack_bf16x2(o[2 * ks + 1][2] * inv, o[2 * ks + 1][3] * inv);
+      const LanePair s0 = swap16(a0, b0), s1 = swap16(a1, b1);
+      *reinterpret_cast<u32x4*>(p.ws + ob + ks * 1024) = odd ? u32x4{s0.lo, s1.lo, b0, b1} : u32x4{a0, a1, s0.hi, s1.hi};
     }
-    if (c.lq == 0) {
-      const f32x2 ml = {m, lsum};
-      *reinterpret_cast<f32x2*>(p.ws + OFF_ATTML + pbase * 8) = ml;
-    }
+  }
+  if (tv && c.lq == 0) {
+    const f32x2 ml = {m, lsum};
+    *reinterpret_cast<f32x2*>(p.ws + OFF_ATTML + pbase * 8) = ml;
   }
 }
 
 // ---------------------------------------------------------------- combine
-// attn_g[t] = sum_ch w_ch O_ch[t] with w_ch = l_ch 2^(m_ch - M) / sum l 2^(m - M). Wave w handles
-// token r + 32(w/2), dims 128(w%2) + 2 lane, +1.
-__device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c) {
-  const int t = c.r + 32 * (c.wave >> 1);
-  if (t >= p.Tv) return;
-  const int d0 = 128 * (c.wave & 1) + 2 * c.lane;
-  unsigned v[NCH];
+// attn_g[t] = sum_ch w_ch O_ch[t] with w_ch = l_ch 2^(m_ch - M) / sum l 2^(m - M). Rank r combines
+// fragment r of the head's output (token tile r / 8, k-step r % 8): a lane owns one 16-byte slot
+// (token 16 (r / 8) + lane / 4, 8 dims). Wave w takes chunks 8w..8w+7; waves 1-3 hand their partials
+// (weighted sum, max, weight) to wave 0 through LDS, counted in control word 9.
+__device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c, int li) {
+  const int tt = c.r >> 3, ks = c.r & 7;
+  if (16 * tt >= p.Tv) return;
+  const int t = 16 * tt + (c.lane >> 2);
+  constexpr int NC = NCH / NCW;
+  u32x4 v[NC];
+  u32x2 ml[NC];
 #pragma unroll
-  for (int ch = 0; ch < NCH; ch++)
-    v[ch] = __builtin_amdgcn_raw_buffer_load_b32(c.ws, OFF_ATTP + (((c.g * NCH + ch) * TP + t) * HD + d0) * 2, 0,
-                                                 kCpSc1);
-  const u32x2 ml = ldb64<kCpSc1>(c.ws, c.lane < NCH ? OFF_ATTML + ((c.g * NCH + c.lane) * TP + t) * 8 : OOB);
-  const float mc = c.lane < NCH ? as_f32(ml[0]) : -1e30f;
-  const float lc = c.lane < NCH ? as_f32(ml[1]) : 0.f;
-  const float M = wave_max(mc);
-  const float w = lc * exp2f(mc - M);
-  const float wgt = w / wave_sum(w);
-  float a0 = 0.f, a1 = 0.f;
+  for (int i = 0; i < NC; i++) {
+    const int ch = NC * c.wave + i;
+    v[i] = ldb128<kCpSc1>(c.ws, OFF_ATTP + ((c.g * NCH + ch) * (TP / 16) + tt) * 8192 + ks * 1024 + c.lane * 16);
+    ml[i] = ldb64<kCpSc1>(c.ws, t < p.Tv ? OFF_ATTML + ((c.g * NCH + ch) * TP + t) * 8 : OOB);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first use
+  float mw = -1e30f;
 #pragma unroll
-  for (int ch = 0; ch < NCH; ch++) {
-    const float wc = as_f32(__builtin_amdgcn_readlane(as_u32(wgt), ch));
-    if (wc != 0.f) {  // empty chunks hold no partial
-      a0 = fmaf(wc, bf_lo(v[ch]), a0);
-      a1 = fmaf(wc, bf_hi(v[ch]), a1);
+  for (int i = 0; i < NC; i++) mw = fmaxf(mw, as_f32(ml[i][0]));
+  float lw = 0.f, u[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) u[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NC; i++) {
+    const float w = as_f32(ml[i][1]) * exp2f(as_f32(ml[i][0]) - mw);
+    lw += w;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const unsigned d = w != 0.f ? v[i][e] : 0u;  // empty chunks (and tokens past Tv) hold no partial
+      u[2 * e] = fmaf(w, bf_lo(d), u[2 * e]);
+      u[2 * e + 1] = fmaf(w, bf_hi(d), u[2 * e + 1]);
     }
   }
-  *reinterpret_cast<unsigned*>(p.ws + OFF_ATTN + c.g * (TP * HD * 2) + frag_off(8, t, d0)) = pack_bf16x2(a0, a1);
+  float* xl = reinterpret_cast<float*>(fa_lds + L_COMB) + c.lane * 10;  // + 640 (w - 1)
+  unsigned* cnt = reinterpret_cast<unsigned*>(fa_lds + L_CTL) + 9;
+  if (c.wave > 0) {
+    float* xw = xl + 640 * (c.wave - 1);
+#pragma unroll
+    for (int e = 0; e < 8; e++) xw[e] = u[e];
+    xw[8] = mw;
+    xw[9] = lw;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (c.lane == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return;
+  }
+  for (unsigned it = 0;; ++it) {
+    if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= 3u * (unsigned)(li + 1) || ctl_ld(6)) break;
+    if (it > kSpinCap) {
+      ctl_st(6, 1u);
+      if (c.lane == 0) atomicOr(c.err, kErrSpin);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");
+  float M = mw;
+#pragma unroll
+  for (int w = 0; w < NCW - 1; w++) M = fmaxf(M, xl[640 * w + 8]);
+  float f = exp2f(mw - M), L = lw * f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) u[e] *= f;
+#pragma unroll
+  for (int w = 0; w < NCW - 1; w++) {
+    const float* xw = xl + 640 * w;
+    f = exp2f(xw[8] - M);
+    L = fmaf(xw[9], f, L);
+#pragma unroll
+    for (int e = 0; e < 8; e++) u[e] = fmaf(xw[e], f, u[e]);
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  u32x4 out;
+#pragma unroll
+  for (int e = 0; e < 4; e++) out[e] = pack_bf16x2(u[2 * e] * inv, u[2 * e + 1] * inv);
+  *reinterpret_cast<u32x4*>(p.ws + OFF_ATTN + c.g * (TP * HD * 2) + (tt * 8 + ks) * 1024 + c.lane * 16) = out;
 }
 
 // ---------------------------------------------------------------- O projection (K-window g)
@@ -985,7 +1108,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
   Ctx c;
   const int tid = threadIdx.x;
   c.lane = tid & 63;
-  c.wave = tid >> 6;
+  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: derived offsets stay scalar
   c.lr = c.lane & 15;
   c.lq = c.lane >> 4;
   c.g = blockIdx.x & 7;
@@ -1066,14 +1189,14 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       launder(c);
       mark(p, c, 9, t0);
       stamp(c, 4);
-      stage_att(p, c, l, pb + PG::K);
+      stage_att(p, c, l, pb + PG::K, li);
       stamp(c, 5);
       mark(p, c, 2, t0);
       xcd_sync(p, c);
       launder(c);
       mark(p, c, 9, t0);
       stamp(c, 6);
-      stage_comb(p, c);
+      stage_comb(p, c, li);
       stamp(c, 7);
       mark(p, c, 3, t0);
       xcd_sync(p, c);

@@ -483,6 +483,7 @@ __device__ __forceinline__ void xread(const Ctx& c, int buf, int t, unsigned par
 #pragma unroll
     for (int k = 0; k < 4; k++) v[gg][k] = ldb128<kCpSc1>(c.ws, b0 + (gg * TP * D + 256 * k) * 4);
   for (unsigned it = 0;; ++it) {
+    if (c.tr && c.lane == 0) c.tr[ts == 26 ? 31 : 27] = it;  // traced layer: re-read rounds so far
     unsigned bad = 0;
 #pragma unroll
     for (int gg = 0; gg < NX; gg++)

@@ -1171,6 +1171,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       const float* mod_in = p.mods + ((size_t)li * 2 + 0) * 3 * D;
       const float* mod_post = p.mods + ((size_t)li * 2 + 1) * 3 * D;
       stamp(c, 0);
+      const unsigned long long clk0 = c.tr ? __builtin_amdgcn_s_memtime() : 0ull;  // traced layer: shader clock
       if (nw) {
         if (l == 0)
           stage_norm<0>(p, c, 1, 0u, nullptr, mod_in, mod_in + D, 0.f);
@@ -1223,6 +1224,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       stamp(c, 13);
       stage_dn<FP8>(p, c, l, pb + PG::DN, par);
       stamp(c, 14);
+      if (c.tr && c.lane == 0) c.tr[28] = __builtin_amdgcn_s_memtime() - clk0;
       mark(p, c, 7, t0);
     }
     if (nw) {

@@ -905,7 +905,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
   // O^T / l (bf16) in the O projection's operand order: fragment ks of this token tile holds dims
   // 32ks..32ks+31, slot (token, q) dims 32ks + 8q..+7. A lane holds dims 16dt + 4lq + i of token lr,
   // so slot q = lq/2 + 2 (lq%2) of tiles (2ks, 2ks+1) is completed by the lane ^ 16 partner's four
-  // dims (one swap per dword), and every store writes one whole 1 KB fragment.
+  // dims (one swap per dword), and every store writes one whole 1 KB fragment (its valid rows).
   {
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
     const bool odd = c.lq & 1;
@@ -918,7 +918,8 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
       const unsigned b0 = pack_bf16x2(o[2 * ks + 1][0] * inv, o[2 * ks + 1][1] * inv);
       const unsigned b1 = pack_bf16x2(o[2 * ks + 1][2] * inv, o[2 * ks + 1][3] * inv);
       const LanePair s0 = swap16(a0, b0), s1 = swap16(a1, b1);
-      *reinterpret_cast<u32x4*>(p.ws + ob + ks * 1024) = odd ? u32x4{s0.lo, s1.lo, b0, b1} : u32x4{a0, a1, s0.hi, s1.hi};
+      if (tv)  // rows past Tv are never read (the combine gives them weight 0)
+        *reinterpret_cast<u32x4*>(p.ws + ob + ks * 1024) = odd ? u32x4{s0.lo, s1.lo, b0, b1} : u32x4{a0, a1, s0.hi, s1.hi};
     }
   }
   if (tv && c.lq == 0) {

@@ -41,6 +41,15 @@ def test_pi05_edge_shapes(gpu, Lp, Tv, S):
     _check(P.make_case(NL=2, Lp=Lp, Tv=Tv, S=S, seed=Lp + Tv), gpu)
 
 
+@pytest.mark.parametrize("Lp,Tv", [(13, 15), (200, 16), (994, 17), (13, 31), (200, 32), (994, 48), (13, 49),
+                                   (994, 63)])
+def test_pi05_token_tile_boundaries(gpu, Lp, Tv):
+    """Tv on either side of the 16-token tiles (the combine skips tiles past Tv, the attention
+    partials skip rows past Tv) and Lp with this step's first key inside an 8-key V^T slot (13, 994)
+    or on a slot boundary (200); Lp = 994 with Tv = 48 / 63 gives two 32-key blocks per rank."""
+    _check(P.make_case(NL=1, Lp=Lp, Tv=Tv, S=2, seed=7 * Lp + Tv), gpu)
+
+
 def test_pi05_deterministic(gpu):
     c = P.make_case(NL=2, Lp=300, Tv=50, S=2)
     g = P.gpu_tensors(c, gpu)

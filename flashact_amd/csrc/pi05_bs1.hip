@@ -943,7 +943,9 @@ __device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c, int li
 #pragma unroll
   for (int i = 0; i < NC; i++) {
     const int ch = NC * c.wave + i;
-    v[i] = ldb128<kCpSc1>(c.ws, OFF_ATTP + ((c.g * NCH + ch) * (TP / 16) + tt) * 8192 + ks * 1024 + c.lane * 16);
+    // rows past Tv were never written: their loads are skipped (out of range returns zeros)
+    v[i] = ldb128<kCpSc1>(c.ws, t < p.Tv ? OFF_ATTP + ((c.g * NCH + ch) * (TP / 16) + tt) * 8192 + ks * 1024 + c.lane * 16
+                                         : OOB);
     ml[i] = ldb64<kCpSc1>(c.ws, t < p.Tv ? OFF_ATTML + ((c.g * NCH + ch) * TP + t) * 8 : OOB);
   }
   __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first use

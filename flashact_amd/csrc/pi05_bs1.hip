@@ -527,27 +527,29 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int bu
   }
   f32x4 x[4];
   if (MODE == 0) {
-    float xa[AD];
+    // x = W_ain x_t + b_ain from coalesced 1 KB reads of W_ain [1024][32]: read j covers rows
+    // 8j..8j+7 (lane L: row 8j + L/8, inputs 4 (L%8)..+3), an 8-lane DPP sum finishes each row,
+    // whose value goes through this wave's residual rows in LDS to the lane layout below.
+    const f32x4 xa = *reinterpret_cast<const f32x4*>(xt + 4 * (c.lane & 7));
+    const float* W = p.w_ain + 4 * c.lane;
+#pragma unroll 1
+    for (int j0 = 0; j0 < D / 8; j0 += 8) {
+      f32x4 w[8];
 #pragma unroll
-    for (int a = 0; a < AD; a++) xa[a] = xt[a];
+      for (int j = 0; j < 8; j++) w[j] = *reinterpret_cast<const f32x4*>(W + (size_t)(j0 + j) * 8 * AD);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        float s = w[j][0] * xa[0] + w[j][1] * xa[1] + w[j][2] * xa[2] + w[j][3] * xa[3];
+        s = dpp_f32<0xB1>(s) + s;   // lane ^ 1
+        s = dpp_f32<0x4E>(s) + s;   // lane ^ 2
+        s = dpp_f32<0x141>(s) + s;  // the other quad of the 8-lane group
+        if ((c.lane & 7) == 0) xres[8 * (j0 + j) + (c.lane >> 3)] = s;
+      }
+    }
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int d = 4 * c.lane + 256 * k;
-      f32x4 wv[4][8];
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int q = 0; q < 8; q++) wv[i][q] = *reinterpret_cast<const f32x4*>(p.w_ain + (d + i) * AD + 4 * q);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(p.b_ain + d);
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        float s = b[i];
-#pragma unroll
-        for (int q = 0; q < 8; q++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) s = fmaf(wv[i][q][e], xa[4 * q + e], s);
-        x[k][i] = s;
-      }
+      x[k] = *reinterpret_cast<const f32x4*>(xres + d) + *reinterpret_cast<const f32x4*>(p.b_ain + d);
     }
   } else {
     u32x4 v[NX][4];

@@ -36,7 +36,7 @@ MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 # L2 <-> memory bytes of one pi05_denoise_bs1 launch at this workload, from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE passes scaled by a 1 GiB device copy (profiles/pi05_denoise_bs1_traffic.md). Counters
 # cannot be read inside a timed run, so the figure is the last measured one for this kernel.
-TRAFFIC_BYTES = {"fetch": 15_927_614_088, "write": 2_817_633_904}
+TRAFFIC_BYTES = {"fetch": 15_598_287_816, "write": 2_487_234_976}
 
 
 # Stage counters (stage_cycles, workgroup 0, 100 MHz ticks) of each kernel: counter index -> stage.

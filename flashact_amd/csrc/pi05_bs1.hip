@@ -15,24 +15,27 @@
 //         polls the XCD's 128 slots (one 16-byte load per lane).
 //   {exchange} = the O / down partial sums are the only data crossing XCDs. Producers store
 //         them with the exchange parity in the lowest mantissa bit of every fp32 value; the
-//         consumers (N1 / N2 / final norm) poll the data itself until every value carries the
-//         current parity, so no grid-wide barrier exists anywhere.
+//         consumers (N1 / N2 / final norm) poll one 16-byte hint per source XCD (its last-written
+//         values), then read everything and re-read any value whose parity is still stale, so no
+//         grid-wide barrier exists anywhere.
 //   (the reference runs 9 grid-wide barriers per layer: src/pi05/mk6.cu:301-497).
-//   N1/N2/FINAL: waves 0/1 of rank r own tokens r / r+32: sum the 8 XCD partials, gated
-//        residual (the residual x and x_t live in LDS), adaRMS -> bf16 operand (or the final
-//        action projection and Euler update).
+//   N1/N2/FINAL: waves 0/1 of rank r own tokens r / r+32: sum the 8 XCD partials (layer 0 of a
+//        step: the action embedding instead), gated residual (the residual x and x_t live in
+//        LDS), adaRMS -> bf16 operand (or the final action projection and Euler update).
 //   QKV: 768 rows per XCD (q rows of head g + all k and v rows), 24 rows per CU, RoPE epilogue.
-//   ATT: head g, keys split into 32 chunks (one per rank). Prefix keys of a chunk's first 32
-//        come from LDS (prefetched by the loader), this step's own keys from XCD-private copies
-//        in MFMA fragment order written by QKV. MFMA S^T = K Q^T, online softmax,
-//        O^T = V^T P^T; normalised partial O (bf16) with (m, l) per chunk.
-//   COMB: flash-decoding combine of the 32 chunk partials -> attn_g (bf16).
+//   ATT: head g, keys split into 32 chunks (one per rank). A chunk's first 32 keys are read
+//        from its LDS ring pages: prefix keys prefetched by the loader, this step's own keys
+//        copied in from the XCD-private copies QKV writes in the same layout. MFMA S^T = K Q^T,
+//        online softmax, O^T = V^T P^T; normalised partial O (bf16, whole operand fragments)
+//        with (m, l) per chunk.
+//   COMB: flash-decoding combine of the 32 chunk partials, one operand fragment of attn_g per
+//        rank (four waves, eight chunks each, meeting in LDS).
 //   O:   W_o[32r..32r+32, 256g..256g+256) x attn_g -> partial o_g.
 //   GU:  32 interleaved gate/up rows per CU -> gelu_tanh(g)*u -> h_g (bf16, XCD-private).
 //   DN:  W_d[32r..32r+32, 512g..512g+512) x h_g -> partial z_g.
 // GEMMs: v_mfma_f32_16x16x32_bf16, weight rows as the A operand (16 rows x 32 k per 1 KB
-// fragment, read from the LDS ring) and the wave's 16 tokens as B (16-byte sc1 loads from the
-// XCD's L2, all issued before the first MFMA).
+// fragment, read from the LDS ring in batches of eight ahead of their MFMAs) and the wave's 16
+// tokens as B (16-byte sc1 loads from the XCD's L2, pipelined in chunks of 8 k-steps).
 #include "fa_device.h"
 #include "../../include/flashact_mi355x.h"
 #include "fa_host.h"

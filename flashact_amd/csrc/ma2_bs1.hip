@@ -357,20 +357,32 @@ __device__ __forceinline__ void stage_satt(const Params& p, const Ctx& c) {
 #pragma unroll
   for (int i = 0; i < 24; i++) {
     const LanePair sq = swap32(as_u32(q[i]), as_u32(q[i])), sk = swap32(as_u32(k[i]), as_u32(k[i]));
-      const float qo = as_f32(lo ? sq.hi : sq.lo), ko = as_f32(lo ? sk.hi : sk.lo);  // lane ^ 32
+    const float qo = as_f32(lo ? sq.hi : sq.lo), ko = as_f32(lo ? sk.hi : sk.lo);  // lane ^ 32
     const float* rope = reinterpret_cast<const float*>(lds + L_ROPE);  // staged by the prologue
     const float cs = rope[(tv ? tau : 0) * 48 + j0 + i], sn = rope[TP * 48 + (tv ? tau : 0) * 48 + j0 + i];
     q[i] = lo ? q[i] * cs - qo * sn : qo * sn + q[i] * cs;
     k[i] = lo ? k[i] * cs - ko * sn : ko * sn + k[i] * cs;
   }
-  unsigned short* l16 = reinterpret_cast<unsigned short*>(lds + L_ATT);
   constexpr uint32_t SQ = 0, SK = 12 * 1024, SV = 24 * 1024;
+  // q and k rows: the lane's 24 dims are three whole 8-dim slots of the fragments (16-byte writes);
+  // V^T is transposed, one element per write (pairing neighbouring tokens through DPP was slower)
+  const uint32_t kr = kperm_row(tau);
+#pragma unroll
+  for (int sl = 0; sl < 3; sl++) {
+    const int d = 24 * g4 + 8 * sl;
+    u32x4 qs, ks;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      qs[e] = tv ? pack_bf16x2(q[8 * sl + 2 * e], q[8 * sl + 2 * e + 1]) : 0u;
+      ks[e] = tv ? pack_bf16x2(k[8 * sl + 2 * e], k[8 * sl + 2 * e + 1]) : 0u;
+    }
+    *reinterpret_cast<u32x4*>(lds + L_ATT + SQ + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
+    *reinterpret_cast<u32x4*>(lds + L_ATT + SK + ((kr >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(kr, d)) = ks;
+  }
+  unsigned short* l16 = reinterpret_cast<unsigned short*>(lds + L_ATT);
 #pragma unroll
   for (int i = 0; i < 24; i++) {
     const int d = 24 * g4 + i;
-    l16[(SQ + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) >> 1] = tv ? bf16_bits(q[i]) : 0;
-    const uint32_t kr = kperm_row(tau);
-    l16[(SK + ((kr >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(kr, d)) >> 1] = tv ? bf16_bits(k[i]) : 0;
     l16[(SV + ((d >> 4) * 2 + (tau >> 5)) * 1024 + frag_pos(d, tau)) >> 1] = tv ? bf16_bits(v[i]) : 0;
   }
   __syncthreads();
@@ -415,11 +427,13 @@ __device__ __forceinline__ void stage_catt(const Params& p, const Ctx& c, const 
       for (int i = 0; i < 4; i++) q[4 * qq + i] = as_f32(r[qq][i]);
   }
   rms96(q);
-  unsigned short* l16 = reinterpret_cast<unsigned short*>(lds + L_ATT);
 #pragma unroll
-  for (int i = 0; i < 24; i++) {
-    const int d = 24 * g4 + i;
-    l16[(((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) >> 1] = tv ? bf16_bits(q[i]) : 0;
+  for (int sl = 0; sl < 3; sl++) {  // the lane's 24 dims are three whole 8-dim fragment slots
+    const int d = 24 * g4 + 8 * sl;
+    u32x4 qs;
+#pragma unroll
+    for (int e = 0; e < 4; e++) qs[e] = tv ? pack_bf16x2(q[8 * sl + 2 * e], q[8 * sl + 2 * e + 1]) : 0u;
+    *reinterpret_cast<u32x4*>(lds + L_ATT + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
   }
   __syncthreads();
   if (16 * c.w >= p.Tv) return;

@@ -364,12 +364,24 @@ __device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, const YSr
     }
     __syncthreads();  // the previous item's readers are done with LDS
     unsigned short* lq16 = reinterpret_cast<unsigned short*>(lds);
+    // q and k rows: the lane's 24 dims are three whole 8-dim fragment slots (16-byte writes); V^T
+    // is transposed, one element per write
+    const uint32_t kr = kperm_row(tau);
+#pragma unroll
+    for (int sl = 0; sl < 3; sl++) {
+      const int d = 24 * g4 + 8 * sl;
+      u32x4 qs, ks;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        qs[e] = tv ? pack_bf16x2(q[8 * sl + 2 * e], q[8 * sl + 2 * e + 1]) : 0u;
+        ks[e] = tv ? pack_bf16x2(k[8 * sl + 2 * e], k[8 * sl + 2 * e + 1]) : 0u;
+      }
+      *reinterpret_cast<u32x4*>(lds + S_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
+      *reinterpret_cast<u32x4*>(lds + S_K + ((kr >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(kr, d)) = ks;
+    }
 #pragma unroll
     for (int i = 0; i < 24; i++) {
       const int d = 24 * g4 + i;
-      lq16[(S_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) >> 1] = tv ? bf16_bits(q[i]) : 0;
-      const uint32_t kr = kperm_row(tau);
-      lq16[(S_K + ((kr >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(kr, d)) >> 1] = tv ? bf16_bits(k[i]) : 0;
       lq16[(S_V + ((d >> 4) * 2 + (tau >> 5)) * 1024 + frag_pos(d, tau)) >> 1] = tv ? bf16_bits(v[i]) : 0;
     }
     __syncthreads();
@@ -440,11 +452,13 @@ __device__ __forceinline__ void stage_catt(const Params& p, rsrc_t ws, int l, co
     }
     float (&q)[24] = qq[0];
     rms96(q);
-    unsigned short* lq16 = reinterpret_cast<unsigned short*>(lds);
 #pragma unroll
-    for (int i = 0; i < 24; i++) {
-      const int d = 24 * g4 + i;
-      lq16[(C_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) >> 1] = tv ? bf16_bits(q[i]) : 0;
+    for (int sl = 0; sl < 3; sl++) {  // the lane's 24 dims are three whole 8-dim fragment slots
+      const int d = 24 * g4 + 8 * sl;
+      u32x4 qs;
+#pragma unroll
+      for (int e = 0; e < 4; e++) qs[e] = tv ? pack_bf16x2(q[8 * sl + 2 * e], q[8 * sl + 2 * e + 1]) : 0u;
+      *reinterpret_cast<u32x4*>(lds + C_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
     }
     unsigned vmask[4][4];
 #pragma unroll

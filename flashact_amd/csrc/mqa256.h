@@ -135,13 +135,19 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
       f32x4 s[2][8];
 #pragma unroll
       for (int kt8 = 0; kt8 < 8; kt8++) {
+        // the key tile's 8 fragments are read ahead of its 16 MFMAs (read one by one, every MFMA
+        // pair would wait out an LDS round trip)
+        u32x4 kf[8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) kf[ks] = lds128((kt8 * 8 + ks) * 1024 + lane * 16);
+        __builtin_amdgcn_sched_barrier(0);
         f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
-          const u32x4 kf = lds128((kt8 * 8 + ks) * 1024 + lane * 16);
-          a0 = mfma16(kf, qf[0][ks], a0);
-          a1 = mfma16(kf, qf[1][ks], a1);
+          a0 = mfma16(kf[ks], qf[0][ks], a0);
+          a1 = mfma16(kf[ks], qf[1][ks], a1);
         }
+        __builtin_amdgcn_sched_barrier(0);
         s[0][kt8] = a0;
         s[1][kt8] = a1;
       }
@@ -191,14 +197,17 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
       }
 #pragma unroll
       for (int dt = 0; dt < 16; dt++) {
+        u32x4 va[4];  // the dim tile's 4 V^T fragments, read ahead of its 8 MFMAs
+#pragma unroll
+        for (int sp = 0; sp < 4; sp++) va[sp] = lds128((64 + dt * 4 + sp) * 1024 + lane * 16);
+        __builtin_amdgcn_sched_barrier(0);
         f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int sp = 0; sp < 4; sp++) {
-          u32x4 va = lds128((64 + dt * 4 + sp) * 1024 + lane * 16);
 #pragma unroll
-          for (int e = 0; e < 4; e++) va[e] &= vmask[sp][e];
-          o0 = mfma16(va, pb[0][sp], o0);
-          o1 = mfma16(va, pb[1][sp], o1);
+          for (int e = 0; e < 4; e++) va[sp][e] &= vmask[sp][e];
+          o0 = mfma16(va[sp], pb[0][sp], o0);
+          o1 = mfma16(va[sp], pb[1][sp], o1);
         }
         if (st[0])
           st_b64(ws, (uint32_t)(L.attp + (prow[0] * HD + 16 * dt + 4 * lq) * 2),

@@ -181,23 +181,30 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
     __syncthreads();  // step s landed for every wave; every wave is done with step s - 1
     if (s + 1 < ns) issue(s + 1);
     const uint32_t base = (uint32_t)(s & 1) * S::STEP;
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
-      u32x4 a[WM], b[WN];
+    // fragments of k sub-step ks + 1 are read while the MFMAs of ks run (double-buffered)
+    u32x4 a[2][WM], b[2][WN];
+    auto rd = [&](int ks, int h) {
 #pragma unroll
       for (int i = 0; i < WM; i++) {
         const int mb = wm * WM + i;  // 16-row block of A
-        a[i] = lds128(base + (16 * (mb >> 2) + lr) * S::PITCH + (mb & 3) * 256 + ks * 64 + lq * 16);
+        a[h][i] = lds128(base + (16 * (mb >> 2) + lr) * S::PITCH + (mb & 3) * 256 + ks * 64 + lq * 16);
       }
 #pragma unroll
       for (int j = 0; j < WN; j++) {
         const int nb = wn * WN + j;
-        b[j] = lds128(base + (16 * (S::GA + (nb >> 2)) + lr) * S::PITCH + (nb & 3) * 256 + ks * 64 + lq * 16);
+        b[h][j] = lds128(base + (16 * (S::GA + (nb >> 2)) + lr) * S::PITCH + (nb & 3) * 256 + ks * 64 + lq * 16);
       }
+    };
+    rd(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+      if (ks + 1 < 4) rd(ks + 1, (ks + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < WN; j++)
 #pragma unroll
-        for (int i = 0; i < WM; i++) acc[j][i] = mfma16(b[j], a[i], acc[j][i]);
+        for (int i = 0; i < WM; i++) acc[j][i] = mfma16(b[ks & 1][j], a[ks & 1][i], acc[j][i]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   __syncthreads();  // the ring is free for the next tile

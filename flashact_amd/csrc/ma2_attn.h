@@ -32,9 +32,13 @@ __device__ __forceinline__ void attend(const u32x4 (&qf)[3], uint32_t kbase, uin
   f32x4 s[NKT];
 #pragma unroll
   for (int kt = 0; kt < NKT; kt++) {
+    u32x4 kf[3];  // read ahead of the key tile's MFMAs
+#pragma unroll
+    for (int ks = 0; ks < 3; ks++) kf[ks] = lds128(kbase + (kt * 3 + ks) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 3; ks++) a = mfma16(lds128(kbase + (kt * 3 + ks) * 1024 + lane * 16), qf[ks], a);
+    for (int ks = 0; ks < 3; ks++) a = mfma16(kf[ks], qf[ks], a);
     s[kt] = a;
   }
   float m_ = -1e30f;
@@ -66,13 +70,16 @@ __device__ __forceinline__ void attend(const u32x4 (&qf)[3], uint32_t kbase, uin
   const float inv = 1.0f / ps;
 #pragma unroll
   for (int dt = 0; dt < 6; dt++) {
+    u32x4 va[NKT / 2];  // read ahead of the dim tile's MFMAs
+#pragma unroll
+    for (int sp = 0; sp < NKT / 2; sp++) va[sp] = lds128(vbase + (dt * (NKT / 2) + sp) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sp = 0; sp < NKT / 2; sp++) {
-      u32x4 va = lds128(vbase + (dt * (NKT / 2) + sp) * 1024 + lane * 16);
 #pragma unroll
-      for (int e = 0; e < 4; e++) va[e] &= vmask[sp][e];
-      acc = mfma16(va, pb[sp], acc);
+      for (int e = 0; e < 4; e++) va[sp][e] &= vmask[sp][e];
+      acc = mfma16(va[sp], pb[sp], acc);
     }
     o[dt] = acc * inv;
   }

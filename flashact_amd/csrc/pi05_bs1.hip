@@ -811,6 +811,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) kf[ks] = ldb128<kCpPlain>(c.kc, rb + ks * 64);
       }
+      __builtin_amdgcn_sched_barrier(0);  // the tile's fragments are all requested before its MFMAs
       f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 8; ks++) a = mfma16(kf[ks], qf[ks], a);
@@ -896,6 +897,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
           }
         }
       }
+      __builtin_amdgcn_sched_barrier(0);  // the half's V^T fragments are all requested before its MFMAs
 #pragma unroll
       for (int d8 = 0; d8 < 8; d8++) {
         const int dt = half * 8 + d8;

@@ -175,6 +175,11 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
+// 2^x as the bare v_exp_f32, for softmax weights and their rescale factors: a result below 2^-126
+// comes out as zero or a flushed value instead of an exact denormal (exp2f adds a range fix-up of
+// four more instructions per call for that case). Weights that small vanish against the row sum.
+__device__ __forceinline__ float exp2_w(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // ---------------------------------------------------------------- barriers
 struct Sync {
   uint64_t* xline;  // this XCD's flag line, one slot per rank

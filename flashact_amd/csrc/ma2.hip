@@ -519,7 +519,7 @@ __device__ __forceinline__ void stage_comb(const Params& p, rsrc_t ws) {
         if (c0 + c >= nkc) break;
         const float mc = as_f32(ml[c][0]), lc = as_f32(ml[c][1]);
         const float mn = fmaxf(Mx, mc);
-        const float sa = exp2f(Mx - mn), sc = lc * exp2f(mc - mn);
+        const float sa = exp2_w(Mx - mn), sc = lc * exp2_w(mc - mn);
         Mx = mn;
         den = den * sa + sc;
         acc[0] = acc[0] * sa + sc * bf_lo(v[c][0]);

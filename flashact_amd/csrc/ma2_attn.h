@@ -60,7 +60,7 @@ __device__ __forceinline__ void attend(const u32x4 (&qf)[3], uint32_t kbase, uin
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        pv[4 * kt + i] = exp2f(s[2 * sp + kt][i] - m_);
+        pv[4 * kt + i] = exp2_w(s[2 * sp + kt][i] - m_);
         ps += pv[4 * kt + i];
       }
     pb[sp] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),

@@ -465,7 +465,7 @@ __device__ __forceinline__ void stage_catt(const Params& p, const Ctx& c, const 
   for (int kt = 0; kt < 2; kt++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      pv[4 * kt + i] = exp2f(s[kt][i] - m_);
+      pv[4 * kt + i] = exp2_w(s[kt][i] - m_);
       ps += pv[4 * kt + i];
     }
   ps = cols_sum(ps);
@@ -513,7 +513,7 @@ __device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c) {
 #pragma unroll
   for (int ch = 0; ch < 16; ch++) {
     if (ch >= nch) break;
-    const float wc = as_f32(ml[ch][1]) * exp2f(as_f32(ml[ch][0]) - M);
+    const float wc = as_f32(ml[ch][1]) * exp2_w(as_f32(ml[ch][0]) - M);
     den += wc;
     a0 = fmaf(wc, bf_lo(v[ch]), a0);
     a1 = fmaf(wc, bf_hi(v[ch]), a1);

@@ -71,12 +71,25 @@ struct EpiQKV {
 
 // ---------------------------------------------------------------- attention partials
 // Item (b, kc, qg): keys [128 kc, 128 kc + 128) of sample b against query tiles 16 qg + w + 4 j
-// (wave w, j < 4, two tiles per pass). The chunk's K rows and V^T columns are copied
-// to LDS once, in MFMA fragment order (64 + 64 fragments). K rows are permuted inside each 32-key
-// span so that the S^T accumulators of key tiles (2 sp, 2 sp + 1) are directly the P^T operand of
-// k-step sp: tile row 4a + i of key tile 2 sp + kt holds key 32 sp + 8 a + 4 kt + i.
+// (wave w, j < 4, two tiles per pass). The chunk's K rows and V^T columns are copied to LDS once,
+// by copies of 4 rows x 256 B (one instruction each, the fast global -> LDS pattern) into blocks
+// at a pitch of 1040 B, so the 16 rows of an MFMA fragment sit in 16 different blocks and a
+// fragment read spreads over all banks:
+//   K block (h, s), s = 16 kt + i: dims [128 h, 128 h + 128) of keys x + 32 sp (sp < 4) with
+//     x = 8 (i / 4) + 4 kt + i % 4; fragment row i of key tile 2 sp + kt is key 32 sp + x, so the
+//     S^T accumulators of key tiles (2 sp, 2 sp + 1) are directly the P^T operand of k-step sp.
+//   V^T block y: dims y + 64 rr (rr < 4), the chunk's 128 keys in order.
 // Keys >= Ltot: S = -inf and their V^T elements are zeroed.
-constexpr uint32_t ATT_LDS = 128 * 1024;
+constexpr uint32_t ATT_PITCH = 1040;
+constexpr uint32_t ATT_VB = 64 * ATT_PITCH;       // first V^T block
+constexpr uint32_t ATT_LDS = 128 * ATT_PITCH;
+
+// Partial O of a 16-row query tile (tile = (b NKC + kc) NQT + qt): 8 blocks of 1 KB, block dp holds
+// dim tiles 2 dp and 2 dp + 1 in MFMA output order. The 16 B at lane (row % 16) + 16 g are dims
+// 32 dp + 4 g .. + 3 (8 B), then 32 dp + 16 + 4 g .. + 3 (8 B), of that row, g < 4.
+__host__ __device__ inline size_t attp_off(size_t tile, int dp, int lane) {
+  return ((tile * 8 + dp) * 64 + lane) * 16;
+}
 
 template <class P>
 __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
@@ -90,135 +103,174 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
   for (int it = vwg(); it < items; it += NWG) {
     const int qg = it % nqg, rest = it / nqg, kc = rest % nkc, b = rest / nkc;
     const int key0 = kc * KCH, kend = min(key0 + KCH, Ltot);
+    const bool full = kend == key0 + KCH;  // no key of the chunk lies past Ltot
     const bf16* kb_ = p.kcache + ((size_t)b * p.NL + l) * p.Lmax * HD;
     const bf16* vb_ = p.vtcache + ((size_t)b * p.NL + l) * HD * p.Lmax;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // the previous item's readers are done with LDS
-#pragma unroll
-    for (int j = 0; j < 32; j++) {
-      const int f = w + 4 * j;
-      if (f < 64) {  // K fragment (key tile kt8 = f / 8, k-step f % 8)
-        const int kt8 = f >> 3, ks = f & 7;
-        int key = key0 + 32 * (kt8 >> 1) + 8 * (lr >> 2) + 4 * (kt8 & 1) + (lr & 3);
-        if (key >= Ltot) key = 0;
-        dma16<true>(kb_ + (size_t)key * HD + ks * 32 + 8 * lq, lds_addr(f * 1024));
-      } else {  // V^T fragment (dim tile dt, 32-key span sp)
-        const int fv = f - 64, dt = fv >> 2, sp = fv & 3;
-        int kg = key0 + 32 * sp + 8 * lq;
-        if (kg >= Ltot) kg = 0;
-        dma16<true>(vb_ + (size_t)(16 * dt + lr) * p.Lmax + kg, lds_addr(f * 1024));
-      }
-    }
-    unsigned vmask[4][4];  // V^T element masks of keys >= kend
-#pragma unroll
-    for (int sp = 0; sp < 4; sp++) {
-      const int nv = min(max(kend - (key0 + 32 * sp + 8 * lq), 0), 8);
-#pragma unroll
-      for (int e = 0; e < 4; e++) vmask[sp][e] = nv >= 2 * e + 2 ? 0xffffffffu : (nv == 2 * e + 1 ? 0xffffu : 0u);
-    }
-    vm_wait<0>();
-    __syncthreads();
-    // two query tiles per pass (qt, qt + 4): every K / V^T fragment read from LDS feeds 2 MFMAs
-#pragma unroll 1
-    for (int jp = 0; jp < QTG / 8; jp++) {
-      const int qt[2] = {QTG * qg + w + 8 * jp, QTG * qg + w + 8 * jp + 4};
-      if (qt[0] >= L.NQT) break;
-      const bool has1 = qt[1] < L.NQT;
-      u32x4 qf[2][8];
+    // q of a pass's two query tiles (qt, qt + 4); a missing second tile repeats the first
+    u32x4 qf[2][8];
+    auto load_q = [&](int jp) {
+      const int q0 = QTG * qg + w + 8 * jp;
+      if (q0 >= L.NQT) return;
 #pragma unroll
       for (int q = 0; q < 2; q++) {
-        const int tq = (q == 1 && !has1) ? qt[0] : qt[q];
+        const int tq = (q == 1 && q0 + 4 >= L.NQT) ? q0 : q0 + 4 * q;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
           qf[q][ks] = ldb128<kCpSc1>(ws, (uint32_t)(L.qf + ((((size_t)b * L.NQT + tq) * 8 + ks) * 64 + lane) * 16));
       }
+    };
+    // K blocks and the first pass's q, then the V^T blocks, which arrive while the first pass
+    // computes S and its softmax (16 copies per wave each; lane: row lq, bytes 16 lr .. + 15).
+    // The V^T copies are issued only after the wait for K and q: the compiler's own waits for q
+    // count only its own loads, not these copies, so a copy issued after q would be waited for
+    // at q's first use.
+#pragma unroll
+    for (int j = 0; j < 16; j++) {  // K block (h, s), f = w + 4 j
+      const int f = w + 4 * j, h = f >> 5, sl = f & 31, kt = sl >> 4, i = sl & 15;
+      int key = key0 + 32 * lq + 8 * (i >> 2) + 4 * kt + (i & 3);
+      if (key >= Ltot) key = 0;
+      dma16<true>(kb_ + (size_t)key * HD + 128 * h + 8 * lr, lds_addr(f * ATT_PITCH));
+    }
+    load_q(0);
+    vm_wait<0>();
+    __syncthreads();  // K of every wave has landed
+#pragma unroll
+    for (int j = 0; j < 16; j++) {  // V^T block y
+      const int y = w + 4 * j;
+      int kg = key0 + 8 * lr;
+      if (kg >= Ltot) kg = 0;
+      dma16<true>(vb_ + (size_t)(y + 64 * lq) * p.Lmax + kg, lds_addr(ATT_VB + y * ATT_PITCH));
+    }
+    // two query tiles per pass (qt, qt + 4): every K / V^T fragment read from LDS feeds 2 MFMAs
+#pragma unroll
+    for (int jp = 0; jp < QTG / 8; jp++) {
+      const int qt[2] = {QTG * qg + w + 8 * jp, QTG * qg + w + 8 * jp + 4};
+      const bool act = qt[0] < L.NQT;
+      if (jp > 0 && !act) break;  // (pass 0 runs its V^T barrier in any case)
+      const bool has1 = qt[1] < L.NQT;
       f32x4 s[2][8];
-#pragma unroll
-      for (int kt8 = 0; kt8 < 8; kt8++) {
-        // the key tile's 8 fragments are read ahead of its 16 MFMAs (read one by one, every MFMA
-        // pair would wait out an LDS round trip)
-        u32x4 kf[8];
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) kf[ks] = lds128((kt8 * 8 + ks) * 1024 + lane * 16);
-        __builtin_amdgcn_sched_barrier(0);
-        f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-          a0 = mfma16(kf[ks], qf[0][ks], a0);
-          a1 = mfma16(kf[ks], qf[1][ks], a1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        s[0][kt8] = a0;
-        s[1][kt8] = a1;
-      }
       float mx[2], psum[2];
       u32x4 pb[2][4];
+      if (act) {
 #pragma unroll
-      for (int q = 0; q < 2; q++) {
-        float m_ = -1e30f;
+        for (int kt8 = 0; kt8 < 8; kt8++) {
+          // the key tile's 8 fragments are read ahead of its 16 MFMAs (read one by one, every MFMA
+          // pair would wait out an LDS round trip)
+          u32x4 kf[8];
 #pragma unroll
-        for (int kt8 = 0; kt8 < 8; kt8++)
+          for (int ks = 0; ks < 8; ks++)
+            kf[ks] = lds128(((ks >> 2) * 32 + (kt8 & 1) * 16 + lr) * ATT_PITCH + (kt8 >> 1) * 256 + (ks & 3) * 64 +
+                            lq * 16);
+          __builtin_amdgcn_sched_barrier(0);
+          f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const int key = key0 + 32 * (kt8 >> 1) + 8 * lq + 4 * (kt8 & 1) + i;
-            s[q][kt8][i] = key < kend ? s[q][kt8][i] * qscale : -1e30f;
-            m_ = fmaxf(m_, s[q][kt8][i]);
+          for (int ks = 0; ks < 8; ks++) {
+            a0 = mfma16(kf[ks], qf[0][ks], a0);
+            a1 = mfma16(kf[ks], qf[1][ks], a1);
           }
-        m_ = cols_max(m_);
-        float ps = 0.f;
-#pragma unroll
-        for (int sp = 0; sp < 4; sp++) {
-          float pv[8];
-#pragma unroll
-          for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              pv[4 * kt + i] = exp2f(s[q][2 * sp + kt][i] - m_);
-              ps += pv[4 * kt + i];
-            }
-          pb[q][sp] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
-                            pack_bf16x2(pv[6], pv[7])};
+          __builtin_amdgcn_sched_barrier(0);
+          s[0][kt8] = a0;
+          s[1][kt8] = a1;
         }
-        ps = cols_sum(ps);
-        mx[q] = m_;
-        psum[q] = ps;
+        if (!full) {  // keys past Ltot (K rows copied from key 0): S = -inf
+#pragma unroll
+          for (int q = 0; q < 2; q++)
+#pragma unroll
+            for (int kt8 = 0; kt8 < 8; kt8++)
+#pragma unroll
+              for (int i = 0; i < 4; i++)
+                if (key0 + 32 * (kt8 >> 1) + 8 * lq + 4 * (kt8 & 1) + i >= kend) s[q][kt8][i] = -1e30f;
+        }
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+          float m_ = -1e30f;
+#pragma unroll
+          for (int kt8 = 0; kt8 < 8; kt8++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) m_ = fmaxf(m_, s[q][kt8][i]);
+          m_ = cols_max(m_) * qscale;  // in log2 units
+          float ps = 0.f;
+#pragma unroll
+          for (int sp = 0; sp < 4; sp++) {
+            float pv[8];
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+              for (int i = 0; i < 4; i++) {
+                pv[4 * kt + i] = exp2_w(fmaf(s[q][2 * sp + kt][i], qscale, -m_));
+                ps += pv[4 * kt + i];
+              }
+            pb[q][sp] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                              pack_bf16x2(pv[6], pv[7])};
+          }
+          ps = cols_sum(ps);
+          mx[q] = m_;
+          psum[q] = ps;
+        }
+      }  // act
+      if (jp == 0) {
+        vm_wait<0>();
+        __syncthreads();  // V^T of every wave has landed
+        if (!full && ((kend - key0) & 7)) {
+          // Keys [kend, ...) of the 8-key group that straddles kend come from cache rows past
+          // Ltot: zero them in V^T so that P = 0 meets a finite value. (Groups wholly past Ltot
+          // were copied from key 0 instead.)
+          const int d = threadIdx.x, gk = (kend - key0) >> 3, nv = (kend - key0) & 7;
+          const uint32_t off = ATT_VB + (d & 63) * ATT_PITCH + (d >> 6) * 256 + gk * 16;
+          u32x4 v = lds128(off);
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[e] &= nv >= 2 * e + 2 ? 0xffffffffu : (nv == 2 * e + 1 ? 0xffffu : 0u);
+          *reinterpret_cast<u32x4*>(lds + off) = v;
+          __syncthreads();
+        }
       }
-      // O^T = V^T P^T, one 16-dim tile at a time, stored as soon as it is complete: lane holds
-      // O^T[dim 16 dt + 4 lq + i][query row 16 qt + lr]
-      bool st[2];
-      size_t prow[2];
+      if (!act) continue;
+      if (jp + 1 < QTG / 8) load_q(jp + 1);  // the next pass's q, in flight with this pass's P V
+      // O^T = V^T P^T, one 16-dim tile at a time: lane holds O^T[dim 16 dt + 4 lq + i][query row
+      // 16 qt + lr]. A pair of dim tiles leaves as one 1 KB block of the partial (attp_off).
+      bool st[2], rv[2];
+      size_t prow[2], tile[2];
       float inv[2];
 #pragma unroll
       for (int q = 0; q < 2; q++) {
         const int r = 16 * qt[q] + lr;
-        st[q] = (q == 0 || has1) && r < NH * p.Tv;
-        prow[q] = ((size_t)b * L.NKC + kc) * L.NQT * 16 + r;
+        st[q] = q == 0 || has1;
+        rv[q] = st[q] && r < NH * p.Tv;
+        tile[q] = ((size_t)b * L.NKC + kc) * L.NQT + qt[q];
+        prow[q] = tile[q] * 16 + lr;
         inv[q] = 1.0f / psum[q];
       }
+      u32x2 ev[2];  // the even dim tile's packed rows, stored with the odd one's
 #pragma unroll
       for (int dt = 0; dt < 16; dt++) {
         u32x4 va[4];  // the dim tile's 4 V^T fragments, read ahead of its 8 MFMAs
 #pragma unroll
-        for (int sp = 0; sp < 4; sp++) va[sp] = lds128((64 + dt * 4 + sp) * 1024 + lane * 16);
+        for (int sp = 0; sp < 4; sp++)
+          va[sp] = lds128(ATT_VB + (16 * (dt & 3) + lr) * ATT_PITCH + (dt >> 2) * 256 + sp * 64 + lq * 16);
         __builtin_amdgcn_sched_barrier(0);
         f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int sp = 0; sp < 4; sp++) {
-#pragma unroll
-          for (int e = 0; e < 4; e++) va[sp][e] &= vmask[sp][e];
           o0 = mfma16(va[sp], pb[0][sp], o0);
           o1 = mfma16(va[sp], pb[1][sp], o1);
         }
-        if (st[0])
-          st_b64(ws, (uint32_t)(L.attp + (prow[0] * HD + 16 * dt + 4 * lq) * 2),
-                 u32x2{pack_bf16x2(o0[0] * inv[0], o0[1] * inv[0]), pack_bf16x2(o0[2] * inv[0], o0[3] * inv[0])});
-        if (st[1])
-          st_b64(ws, (uint32_t)(L.attp + (prow[1] * HD + 16 * dt + 4 * lq) * 2),
-                 u32x2{pack_bf16x2(o1[0] * inv[1], o1[1] * inv[1]), pack_bf16x2(o1[2] * inv[1], o1[3] * inv[1])});
+        const u32x2 w0 = {pack_bf16x2(o0[0] * inv[0], o0[1] * inv[0]), pack_bf16x2(o0[2] * inv[0], o0[3] * inv[0])};
+        const u32x2 w1 = {pack_bf16x2(o1[0] * inv[1], o1[1] * inv[1]), pack_bf16x2(o1[2] * inv[1], o1[3] * inv[1])};
+        if (dt & 1) {
+          if (st[0])
+            st_b128(ws, (uint32_t)(L.attp + attp_off(tile[0], dt >> 1, lane)), u32x4{ev[0][0], ev[0][1], w0[0], w0[1]});
+          if (st[1])
+            st_b128(ws, (uint32_t)(L.attp + attp_off(tile[1], dt >> 1, lane)), u32x4{ev[1][0], ev[1][1], w1[0], w1[1]});
+        } else {
+          ev[0] = w0;
+          ev[1] = w1;
+        }
       }
 #pragma unroll
       for (int q = 0; q < 2; q++)
-        if (st[q] && lq == 0) st_b64(ws, (uint32_t)(L.ml + prow[q] * 8), u32x2{as_u32(mx[q]), as_u32(psum[q])});
+        if (rv[q] && lq == 0) st_b64(ws, (uint32_t)(L.ml + prow[q] * 8), u32x2{as_u32(mx[q]), as_u32(psum[q])});
     }
   }
 }
@@ -231,6 +283,7 @@ template <class P>
 __device__ __forceinline__ void stage_comb(const P& p, rsrc_t ws) {
   const auto& L = p.L;
   const int lane = lane_id(), sub = lane >> 4, l16 = lane & 15;
+  const int dp = l16 >> 1, jh = l16 & 1;  // lane: dims 32 dp + 8 jh .. + 7 and 32 dp + 16 + 8 jh .. + 7
   const int Ltot = p.Lp + p.Tv, nkc = (Ltot + KCH - 1) / KCH;
   const int rows = p.B * NH * p.Tv;
 #pragma unroll 1
@@ -241,6 +294,7 @@ __device__ __forceinline__ void stage_comb(const P& p, rsrc_t ws) {
     const int b = Rc / (NH * p.Tv), r = Rc - b * NH * p.Tv, h = r / p.Tv, t = r - h * p.Tv;
     const size_t cstride = (size_t)L.NQT * 16;  // rows per chunk
     const size_t row0 = (size_t)b * L.NKC * cstride + r;
+    const size_t tile0 = (size_t)b * L.NKC * L.NQT + (r >> 4);
     float Mx = -1e30f, den = 0.f;
     f32x4 acc[4] = {};
 #pragma unroll 1
@@ -254,14 +308,16 @@ __device__ __forceinline__ void stage_comb(const P& p, rsrc_t ws) {
         ml[c] = ldb64<kCpSc1>(ws, ok ? (uint32_t)(L.ml + prow * 8) : (uint32_t)L.ml);
 #pragma unroll
         for (int k = 0; k < 2; k++)
-          v[c][k] = ldb128<kCpSc1>(ws, ok ? (uint32_t)(L.attp + (prow * HD + 16 * l16 + 8 * k) * 2) : (uint32_t)L.attp);
+          v[c][k] = ldb128<kCpSc1>(ws, ok ? (uint32_t)(L.attp + attp_off(tile0 + (size_t)(c0 + c) * L.NQT, dp,
+                                                                          (r & 15) + 16 * (2 * jh + k)))
+                                          : (uint32_t)L.attp);
       }
 #pragma unroll
       for (int c = 0; c < 8; c++) {
         if (c0 + c >= nkc) break;
         const float mc = as_f32(ml[c][0]), lc = as_f32(ml[c][1]);
         const float mn = fmaxf(Mx, mc);
-        const float sa = exp2f(Mx - mn), sc = lc * exp2f(mc - mn);
+        const float sa = exp2_w(Mx - mn), sc = lc * exp2_w(mc - mn);
         Mx = mn;
         den = den * sa + sc;
 #pragma unroll
@@ -279,13 +335,13 @@ __device__ __forceinline__ void stage_comb(const P& p, rsrc_t ws) {
     if (valid) {
       const float inv = 1.0f / den;
       const int m = b * p.Tv + t;
+      // acc[2 k + e]: dims 32 dp + 16 e + 8 jh + 4 k .. + 3
 #pragma unroll
-      for (int k = 0; k < 2; k++) {
-        const u32x4 o = {pack_bf16x2(acc[2 * k][0] * inv, acc[2 * k][1] * inv),
-                         pack_bf16x2(acc[2 * k][2] * inv, acc[2 * k][3] * inv),
-                         pack_bf16x2(acc[2 * k + 1][0] * inv, acc[2 * k + 1][1] * inv),
-                         pack_bf16x2(acc[2 * k + 1][2] * inv, acc[2 * k + 1][3] * inv)};
-        st_b128(ws, (uint32_t)(L.attn + ((size_t)m * QD + h * HD + 16 * l16 + 8 * k) * 2), o);
+      for (int e = 0; e < 2; e++) {
+        const u32x4 o = {pack_bf16x2(acc[e][0] * inv, acc[e][1] * inv), pack_bf16x2(acc[e][2] * inv, acc[e][3] * inv),
+                         pack_bf16x2(acc[2 + e][0] * inv, acc[2 + e][1] * inv),
+                         pack_bf16x2(acc[2 + e][2] * inv, acc[2 + e][3] * inv)};
+        st_b128(ws, (uint32_t)(L.attn + ((size_t)m * QD + h * HD + 32 * dp + 16 * e + 8 * jh) * 2), o);
       }
     }
   }

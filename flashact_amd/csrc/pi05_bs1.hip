@@ -830,7 +830,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
       }
     bmax = cols_max(bmax);
     const float mnew = fmaxf(m, bmax);
-    const float alpha = exp2f(m - mnew);
+    const float alpha = exp2_w(m - mnew);
     m = mnew;
     float psum = 0.f;
     unsigned pk[4];
@@ -839,7 +839,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
       float pv[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        pv[i] = exp2f(s[kt][i] - m);
+        pv[i] = exp2_w(s[kt][i] - m);
         psum += pv[i];
       }
       pk[kt * 2 + 0] = pack_bf16x2(pv[0], pv[1]);
@@ -964,6 +964,7 @@ __device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c, int li
   for (int e = 0; e < 8; e++) u[e] = 0.f;
 #pragma unroll
   for (int i = 0; i < NC; i++) {
+    // exp2f, not the bare exp2_w: with exp2_w this stage measured 0.85 us slower per layer
     const float w = as_f32(ml[i][1]) * exp2f(as_f32(ml[i][0]) - mw);
     lw += w;
 #pragma unroll

@@ -315,7 +315,7 @@ __device__ __forceinline__ void load24(rsrc_t ws, const YSrc& y, int MP, int m, 
   } else {
 #pragma unroll
     for (int i = 0; i < 6 * NT; i++) acc[i] = *reinterpret_cast<const f32x4*>(y.bias + cols[i]);
-    add_parts<6 * NT, (NT == 1 ? 4 : 1)>(ws, y.parts, y.ks, MP, y.N, m, cols, acc);
+    add_parts<6 * NT, (NT == 1 ? 6 : 1)>(ws, y.parts, y.ks, MP, y.N, m, cols, acc);
   }
 #pragma unroll
   for (int t = 0; t < NT; t++)
@@ -410,55 +410,64 @@ __device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, const YSr
 }
 
 // Cross attention item (b, h, kc): context keys [128 kc, 128 kc + 128) of head h. The chunk's K
-// rows and V^T columns are copied to LDS (24 + 24 fragments); wave w prepares the query rows
-// 16w..16w+15 (sum of CQ partials + b_cq, per-head RMS) and attends with them.
-constexpr uint32_t C_Q = 0, C_K = 12 * 1024, C_V = 36 * 1024;
+// rows and V^T columns are copied to LDS (24 + 24 fragments); wave i of the item prepares the query
+// rows 16 i .. 16 i + 15 (sum of the CQ partials + b_cq, per-head RMS) and attends with them. With
+// Tv <= 32 an item needs two waves, and waves 0-1 and 2-3 run two items side by side, each in its
+// own C_ITEM bytes of LDS; otherwise all four waves run one item.
+constexpr uint32_t C_Q = 0, C_K = 12 * 1024, C_V = 36 * 1024, C_ITEM = 60 * 1024;
+static_assert(2 * C_ITEM <= 136 * 1024, "two cross-attention items fit the attention LDS");
 
 template <bool FIX>
 __device__ __forceinline__ void stage_catt(const Params& p, rsrc_t ws, int l, const YSrc& y) {
   const Layout& L = p.L;
   const int w = wave_id(), lane = lane_id(), lr = lane & 15, g4 = lane >> 4;
-  const int nkc = (p.Lk + KCH - 1) / KCH;
+  const int nkc = (p.Lk + KCH - 1) / KCH, items = p.B * NH * nkc;
+  const int wpi = p.Tv <= 32 ? 2 : 4;     // waves per item
+  const int slot = w / wpi, wi = w % wpi;  // item slot of this wave, its index within the item
+  const uint32_t cb = slot * C_ITEM;
 #pragma unroll 1
-  for (int it = vwg(); it < p.B * NH * nkc; it += NWG) {
+  for (int it0 = vwg(); it0 < items; it0 += NWG * (4 / wpi)) {  // every wave takes the same trips
+    const int it = it0 + NWG * slot;
+    const bool act = it < items;
     const int kc = it % nkc, rest = it / nkc, h = rest % NH, b = rest / NH;
     const int key0 = kc * KCH, kvalid = min(KCH, p.Lk - key0);
     const bf16* kb_ = p.kctx + ((size_t)b * p.NL + l) * p.Lkmax * D + HD * h;
     const bf16* vb_ = p.vtctx + (((size_t)b * p.NL + l) * D + HD * h) * p.Lkmax;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // the previous item's readers are done with LDS
-#pragma unroll
-    for (int j = 0; j < 12; j++) {
-      const int f = w + 4 * j;  // 0..47
-      if (f < 24) {             // K fragment (key tile kt = f / 3, k-step f % 3)
-        const int kt = f / 3, ks = f - 3 * kt;
-        int key = key0 + 32 * (kt >> 1) + 8 * (lr >> 2) + 4 * (kt & 1) + (lr & 3);
-        if (key >= p.Lk) key = 0;
-        dma16<false>(kb_ + (size_t)key * D + ks * 32 + 8 * g4, lds_addr(C_K + f * 1024));
-      } else {  // V^T fragment (dim tile dt, span sp)
-        const int fv = f - 24, dt = fv >> 2, sp = fv & 3;
-        int kg = key0 + 32 * sp + 8 * g4;
-        if (kg >= p.Lk) kg = 0;
-        dma16<false>(vb_ + (size_t)(16 * dt + lr) * p.Lkmax + kg, lds_addr(C_V + fv * 1024));
+    if (act) {
+#pragma unroll 1
+      for (int f = wi; f < 48; f += wpi) {
+        if (f < 24) {  // K fragment (key tile kt = f / 3, k-step f % 3)
+          const int kt = f / 3, ks = f - 3 * kt;
+          int key = key0 + 32 * (kt >> 1) + 8 * (lr >> 2) + 4 * (kt & 1) + (lr & 3);
+          if (key >= p.Lk) key = 0;
+          dma16<false>(kb_ + (size_t)key * D + ks * 32 + 8 * g4, lds_addr(cb + C_K + f * 1024));
+        } else {  // V^T fragment (dim tile dt, span sp)
+          const int fv = f - 24, dt = fv >> 2, sp = fv & 3;
+          int kg = key0 + 32 * sp + 8 * g4;
+          if (kg >= p.Lk) kg = 0;
+          dma16<false>(vb_ + (size_t)(16 * dt + lr) * p.Lkmax + kg, lds_addr(cb + C_V + fv * 1024));
+        }
       }
-    }
-    // query rows of this wave
-    const int tau = 16 * w + lr;
-    const bool tv = tau < p.Tv;
-    float qq[1][24];
-    {
-      const int cs[1] = {HD * h + 24 * g4};
-      load24<1, FIX>(ws, y, L.MP, b * p.Tv + (tv ? tau : 0), cs, qq);
-    }
-    float (&q)[24] = qq[0];
-    rms96(q);
+      // query rows of this wave
+      const int tau = 16 * wi + lr;
+      const bool tv = tau < p.Tv;
+      float qq[1][24];
+      {
+        const int cs[1] = {HD * h + 24 * g4};
+        load24<1, FIX>(ws, y, L.MP, b * p.Tv + (tv ? tau : 0), cs, qq);
+      }
+      float (&q)[24] = qq[0];
+      rms96(q);
 #pragma unroll
-    for (int sl = 0; sl < 3; sl++) {  // the lane's 24 dims are three whole 8-dim fragment slots
-      const int d = 24 * g4 + 8 * sl;
-      u32x4 qs;
+      for (int sl = 0; sl < 3; sl++) {  // the lane's 24 dims are three whole 8-dim fragment slots
+        const int d = 24 * g4 + 8 * sl;
+        u32x4 qs;
 #pragma unroll
-      for (int e = 0; e < 4; e++) qs[e] = tv ? pack_bf16x2(q[8 * sl + 2 * e], q[8 * sl + 2 * e + 1]) : 0u;
-      *reinterpret_cast<u32x4*>(lds + C_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
+        for (int e = 0; e < 4; e++) qs[e] = tv ? pack_bf16x2(q[8 * sl + 2 * e], q[8 * sl + 2 * e + 1]) : 0u;
+        *reinterpret_cast<u32x4*>(lds + cb + C_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
+      }
     }
     unsigned vmask[4][4];
 #pragma unroll
@@ -469,14 +478,14 @@ __device__ __forceinline__ void stage_catt(const Params& p, rsrc_t ws, int l, co
     }
     vm_wait<0>();
     __syncthreads();
-    if (16 * w < p.Tv) {
+    if (act && 16 * wi < p.Tv) {
       u32x4 qf[3];
 #pragma unroll
-      for (int ks = 0; ks < 3; ks++) qf[ks] = lds128(C_Q + (w * 3 + ks) * 1024 + lane * 16);
+      for (int ks = 0; ks < 3; ks++) qf[ks] = lds128(cb + C_Q + (wi * 3 + ks) * 1024 + lane * 16);
       float mx, ps;
       f32x4 o[6];
-      attend<8>(qf, C_K, C_V, kvalid, vmask, mx, ps, o);
-      const int t = 16 * w + lr;
+      attend<8>(qf, cb + C_K, cb + C_V, kvalid, vmask, mx, ps, o);
+      const int t = 16 * wi + lr;
       if (t < p.Tv) {
         const size_t prow = (((size_t)b * NH + h) * L.NKC + kc) * MAX_TV + t;
 #pragma unroll

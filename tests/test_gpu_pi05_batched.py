@@ -32,7 +32,10 @@ def test_batched_two_samples(gpu):
     _check(P.make_case(NL=2, Lp=968, Tv=50, S=2, batch=2), gpu)
 
 
-@pytest.mark.parametrize("B,Lp,Tv,S", [(3, 37, 17, 2), (2, 0, 50, 1), (5, 300, 64, 1), (2, 1100, 9, 2)])
+# Lp + Tv: 54, 50, 364, 1109 end inside a 128-key chunk (the last chunk masked, its V^T tail group
+# zeroed), 256 fills every chunk exactly (no masking at all)
+@pytest.mark.parametrize("B,Lp,Tv,S", [(3, 37, 17, 2), (2, 0, 50, 1), (5, 300, 64, 1), (2, 1100, 9, 2),
+                                      (2, 206, 50, 1)])
 def test_batched_edge_shapes(gpu, B, Lp, Tv, S):
     _check(P.make_case(NL=2, Lp=Lp, Tv=Tv, S=S, batch=B, seed=B + Lp + Tv), gpu)
 

@@ -44,7 +44,7 @@ def test_prefill_small(gpu):
     assert torch.count_nonzero(kc[:, :, 200:]) == 0 and torch.count_nonzero(vt[:, :, :, 200:]) == 0
 
 
-@pytest.mark.parametrize("Lp,B", [(1, 1), (17, 2), (129, 1), (300, 2)])
+@pytest.mark.parametrize("Lp,B", [(1, 1), (17, 2), (129, 1), (256, 1), (300, 2)])  # 256: whole key chunks
 def test_prefill_edge_shapes(gpu, Lp, B):
     c = C.make_case(NL=2, Lp=Lp, batch=B, seed=Lp)
     kc, vt = C.run_gpu(c, gpu)

@@ -334,7 +334,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the pi0.5/MolmoAct2 denoise loop is a single-GPU "
-                                   "kernel (batch-DP sharding needs no exchange; see DESIGN.md)", "n_gpus": args.gpus}))
+                                   "kernel; across GPUs the batch would be split, one launch per GPU on its share, "
+                                   "with no exchange inside the loop", "n_gpus": args.gpus}))
         sys.exit(2)
     dev = torch.device("cuda:0")
     if args.copy_bytes > 0:

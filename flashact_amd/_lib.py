@@ -10,11 +10,13 @@ import os
 
 from .build import LIB_PATH
 
-ABI_VERSION = 1
+ABI_VERSION = 2
+STAGE_TICK_HZ = 100_000_000  # FA_STAGE_TICK_HZ: unit of the stage_cycles counters
 
 FA_OK = 0
 FA_DTYPE_BF16 = 0
 FA_DTYPE_FP8_E4M3 = 1
+FA_DTYPE_F16 = 2
 FA_KSTATUS_SPIN_TIMEOUT = 1
 FA_KSTATUS_XCD_MAP = 2
 
@@ -39,6 +41,7 @@ class Pi05Args(ctypes.Structure):
         ("stage_cycles", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("trace", ctypes.c_void_p), ("trace_layer", ctypes.c_int),
+        ("cache_dtype", ctypes.c_int), ("cache_shadow", ctypes.c_void_p), ("cache_shadow_bytes", ctypes.c_size_t),
     ]
 
 
@@ -83,6 +86,7 @@ class DeviceInfo(ctypes.Structure):
 SYMBOLS = [
     ("fa_pi05_denoise", ctypes.c_int, [ctypes.POINTER(Pi05Args), ctypes.c_void_p]),
     ("fa_pi05_workspace_bytes", ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    ("fa_pi05_cache_shadow_bytes", ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     ("fa_pi05_workspace_init", ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     ("fa_pi05_read_status", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint)]),
     ("fa_pi05_max_batch", ctypes.c_int, []),

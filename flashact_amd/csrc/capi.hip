@@ -86,7 +86,7 @@ extern "C" int fa_device_query(int device, fa_device_info* info) {
   info->lds_bytes = (int)prop.sharedMemPerBlock;
   if (hipDeviceGetAttribute(&info->coop_launch, hipDeviceAttributeCooperativeLaunch, device) != hipSuccess)
     info->coop_launch = 0;
-  info->coop_max_blocks = prop.multiProcessorCount;
+  info->coop_max_blocks = fa::pi05_bs1_coop_capacity(device);
   strncpy(info->arch, prop.gcnArchName, sizeof(info->arch) - 1);
   return FA_OK;
 }

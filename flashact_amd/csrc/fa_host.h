@@ -35,6 +35,15 @@ int pi05_denoise_batched(const fa_pi05_args* a, fa_stream_t stream);
 // caches ahead of the denoise launch. Arguments are checked by fa_pi05_denoise.
 int pi05_kv_handoff(const fa_pi05_args* a, fa_stream_t stream);
 
+// fp16 caches (cache_dtype == FA_DTYPE_F16): both caches -> the bf16 shadow ahead of the loop, and the
+// rows the loop (and a hand-off) wrote -> the caller's fp16 caches after it. Elements per cache.
+size_t pi05_cache_elems(int batch, int num_layers, int Lmax);
+int pi05_cache_import(const fa_pi05_args* a, fa_stream_t stream);
+int pi05_cache_export(const fa_pi05_args* a, fa_stream_t stream);
+
+// Co-resident workgroups of the batch-1 pi0.5 kernel on a device (0 if it cannot run there).
+int pi05_bs1_coop_capacity(int device);
+
 // Batch-1 MolmoAct2 launch (XCD-local layout), dispatched from fa_ma2_flow when eligible.
 bool ma2_bs1_eligible(int batch, int Tv, int Lkmax);
 size_t ma2_bs1_workspace_bytes();

@@ -10,6 +10,8 @@
 // stream; stream order stands in for the reference's grid.sync() after the prologue.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "../../include/flashact_mi355x.h"
 #include "fa_device.h"
 #include "fa_host.h"
@@ -52,7 +54,78 @@ __global__ void __launch_bounds__(256) kv_handoff_kernel(const unsigned short* _
   }
 }
 
+// fp16 caches (the reference's, src/pi05/binding.cpp:6, benchmarks/pi05/eval_numerics.py:83-85)
+// -> the bf16 shadow the denoise kernels read: 8 elements per thread and iteration, each
+// fp16 -> fp32 (exact) -> bf16 (round to nearest even).
+__global__ void __launch_bounds__(256) cache_import_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                           size_t n8) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n8; i += (size_t)gridDim.x * blockDim.x) {
+    const u32x4 v = src[i];
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const unsigned w = v[j];
+      const float lo = (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xffffu));
+      const float hi = (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
+      o[j] = pack_bf16x2(lo, hi);
+    }
+    dst[i] = o;
+  }
+}
+
+// fp32 -> fp16 bits, round to nearest even (v_cvt_f16_f32)
+__device__ __forceinline__ unsigned short f16_bits(float f) { return __builtin_bit_cast(unsigned short, (_Float16)f); }
+
+// The rows a launch wrote, bf16 shadow -> the caller's fp16 caches (round to nearest even):
+// kcache rows [r0, r1) and vtcache columns [r0, r1) of every (sample, layer) bl.
+__global__ void __launch_bounds__(256) cache_export_kernel(const unsigned short* __restrict__ kb,
+                                                           const unsigned short* __restrict__ vb,
+                                                           unsigned short* __restrict__ kh,
+                                                           unsigned short* __restrict__ vh, int Lmax, int r0,
+                                                           int nr) {
+  const size_t bl = blockIdx.y;
+  const int n = nr * HD;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const size_t ko = (bl * Lmax + r0) * HD + i;  // row r0 + i / HD, dim i % HD
+    kh[ko] = f16_bits(as_f32((unsigned)kb[ko] << 16));
+    const int d = i / nr, r = i - d * nr;
+    const size_t vo = (bl * HD + d) * Lmax + r0 + r;
+    vh[vo] = f16_bits(as_f32((unsigned)vb[vo] << 16));
+  }
+}
+
 }  // namespace kvh
+
+size_t pi05_cache_elems(int batch, int num_layers, int Lmax) { return (size_t)batch * num_layers * Lmax * kvh::HD; }
+
+int pi05_cache_import(const fa_pi05_args* a, fa_stream_t stream) {
+  using namespace fa::kvh;
+  const size_t n = pi05_cache_elems(a->batch, a->num_layers, a->Lmax);  // per cache, a multiple of 8
+  unsigned char* sh = static_cast<unsigned char*>(a->cache_shadow);
+  const size_t n8 = n / 8;
+  const unsigned blocks = (unsigned)std::min<size_t>((n8 + 255) / 256, 8192);
+  hipLaunchKernelGGL(cache_import_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const u32x4*>(a->kcache), reinterpret_cast<u32x4*>(sh), n8);
+  hipLaunchKernelGGL(cache_import_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const u32x4*>(a->vtcache), reinterpret_cast<u32x4*>(sh + 2 * n), n8);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_pi05_denoise: fp16 cache import: %s", hipGetErrorString(e));
+  return FA_OK;
+}
+
+int pi05_cache_export(const fa_pi05_args* a, fa_stream_t stream) {
+  using namespace fa::kvh;
+  const size_t n = pi05_cache_elems(a->batch, a->num_layers, a->Lmax);
+  const unsigned short* sh = static_cast<const unsigned short*>(a->cache_shadow);
+  const int r0 = a->srows > 0 ? 0 : a->Lp, nr = a->Lp + a->Tv - r0;
+  const unsigned bx = (unsigned)std::min((nr * HD + 255) / 256, 64);
+  hipLaunchKernelGGL(cache_export_kernel, dim3(bx, (unsigned)(a->batch * a->num_layers)), dim3(256), 0,
+                     (hipStream_t)stream, sh, sh + n, static_cast<unsigned short*>(a->kcache),
+                     static_cast<unsigned short*>(a->vtcache), a->Lmax, r0, nr);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_pi05_denoise: fp16 cache export: %s", hipGetErrorString(e));
+  return FA_OK;
+}
 
 int pi05_kv_handoff(const fa_pi05_args* a, fa_stream_t stream) {
   using namespace fa::kvh;
@@ -70,3 +143,8 @@ int pi05_kv_handoff(const fa_pi05_args* a, fa_stream_t stream) {
 }
 
 }  // namespace fa
+
+extern "C" size_t fa_pi05_cache_shadow_bytes(int batch, int num_layers, int Lmax) {
+  if (batch < 1 || num_layers < 1 || Lmax < 16 || (Lmax & 15)) return 0;
+  return 2 * fa::pi05_cache_elems(batch, num_layers, Lmax) * 2;
+}

@@ -616,7 +616,6 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
   const int NL = p.NL;
   const float dt = 1.0f / (float)p.S;
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x < 16) p.stage_cycles[threadIdx.x] = 0;
 #pragma unroll 1
   for (int step = 0; step < p.S; step++) {
 #pragma unroll 1

@@ -237,7 +237,6 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
   const int NL = p.NL;
   const float dt = -1.0f / (float)p.S;
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x < 16) p.stage_cycles[threadIdx.x] = 0;
   GemmArgs gx{reinterpret_cast<const bf16*>(p.ws + L.xn), nullptr, D, D, L.M};
   GemmArgs ga{reinterpret_cast<const bf16*>(p.ws + L.attn), nullptr, QD, QD, L.M};
   GemmArgs gh{reinterpret_cast<const bf16*>(p.ws + L.h), nullptr, FF, FF, L.M};

@@ -1277,6 +1277,22 @@ extern "C" size_t fa_pi05_workspace_bytes(int batch, int Tv, int Lmax) {
 
 extern "C" int fa_pi05_max_batch(void) { return 64; }
 
+// Co-resident workgroups of the batch-1 bf16 kernel on `device`: occupancy per CU (at its thread
+// count and dynamic LDS) times the CU count.
+int fa::pi05_bs1_coop_capacity(int device) {
+  int prev = 0;
+  if (hipGetDevice(&prev) != hipSuccess) return 0;
+  if (device != prev && hipSetDevice(device) != hipSuccess) return 0;
+  int per_cu = 0, cus = 0;
+  const void* kern = (const void*)pi05::pi05_denoise_bs1<false>;
+  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pi05::LDS_BYTES) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, pi05::NTH, pi05::LDS_BYTES) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    per_cu = 0;
+  if (device != prev) (void)hipSetDevice(prev);
+  return per_cu * cus;
+}
+
 extern "C" int fa_pi05_workspace_init(void* workspace, size_t bytes, fa_stream_t stream) {
   if (!workspace || bytes == 0 || (bytes & 15) || (reinterpret_cast<uintptr_t>(workspace) & 255))
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_workspace_init: workspace must be non-null, 256-byte aligned, "
@@ -1348,6 +1364,29 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: KV cache larger than 2 GiB per sample");
   if (a->xt_rows < a->Tv)
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: xt_rows=%d < Tv=%d", a->xt_rows, a->Tv);
+  if (a->cache_dtype == FA_DTYPE_F16) {
+    // The reference's fp16 caches: import into the bf16 shadow, run the bf16 loop on it, export the
+    // rows the loop wrote. Stream order sequences the three.
+    const size_t need = fa_pi05_cache_shadow_bytes(a->batch, a->num_layers, a->Lmax);
+    if (!a->cache_shadow || (reinterpret_cast<uintptr_t>(a->cache_shadow) & 255) || a->cache_shadow_bytes < need)
+      return host::fail(FA_ERR_INVALID_ARG,
+                        "fa_pi05_denoise: fp16 caches need a 256-byte aligned cache_shadow of >= %zu bytes "
+                        "(got %p, %zu bytes)", need, a->cache_shadow, a->cache_shadow_bytes);
+    fa_pi05_args b = *a;
+    unsigned char* sh = static_cast<unsigned char*>(a->cache_shadow);
+    b.kcache = sh;
+    b.vtcache = sh + 2 * pi05_cache_elems(a->batch, a->num_layers, a->Lmax);
+    b.cache_dtype = FA_DTYPE_BF16;
+    b.cache_shadow = nullptr;
+    b.cache_shadow_bytes = 0;
+    int rc = pi05_cache_import(a, stream);
+    if (rc == FA_OK) rc = fa_pi05_denoise(&b, stream);
+    if (rc == FA_OK) rc = pi05_cache_export(a, stream);
+    return rc;
+  }
+  if (a->cache_dtype != FA_DTYPE_BF16)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: cache_dtype=%d is neither FA_DTYPE_BF16 nor FA_DTYPE_F16",
+                      a->cache_dtype);
   if (a->batch > 1) return pi05_denoise_batched(a, stream);
   if (a->workspace_bytes < WS_BYTES)
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: workspace_bytes=%zu < required %u", a->workspace_bytes,

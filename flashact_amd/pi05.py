@@ -2,7 +2,7 @@
 
 ``launch`` keeps the positional signature of the reference's ``mk_v6.launch``
 (src/pi05/binding.cpp:28-37) so harness call sites stay drop-in
-(benchmarks/pi05/eval_numerics.py:333-339, src/pi05/hybrid_model.py:215-221). It forwards
+(benchmarks/pi05/eval_numerics.py:101-107, src/pi05/hybrid_model.py:215-221). It forwards
 device pointers to the C ABI ``fa_pi05_denoise`` (include/flashact_mi355x.h), which enqueues
 ONE cooperative HIP launch for the whole Euler loop on the current torch stream.
 
@@ -12,7 +12,7 @@ Packing helpers mirror the reference's host code:
   precompute_mods ..... src/pi05/hybrid_model.py:111-128 (sinusoid -> time MLP -> adaRMS dense)
   rope_table .......... src/pi05/pack_weights.py:54-58
   compact_kv .......... src/pi05/pack_weights.py:60-70
-  make_caches ......... benchmarks/pi05/eval_numerics.py:314-319 (K rows, V transposed)
+  make_caches ......... benchmarks/pi05/eval_numerics.py:83-87 (K rows, V transposed)
 """
 from __future__ import annotations
 
@@ -184,23 +184,92 @@ def _ptr(t):
     return t.data_ptr()
 
 
+_SHADOW: dict = {}
+
+
+def cache_shadow(device, batch: int, num_layers: int, Lmax: int) -> torch.Tensor:
+    """Per-device cached bf16 shadow for launches on fp16 caches (256-byte aligned)."""
+    dev = torch.device(device)
+    nbytes = int(_lib.lib().fa_pi05_cache_shadow_bytes(batch, num_layers, Lmax))
+    if nbytes == 0:
+        raise ValueError(f"no cache shadow size for batch={batch} num_layers={num_layers} Lmax={Lmax}")
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    sh = _SHADOW.get(key)
+    if sh is None or sh.numel() < nbytes:
+        sh = torch.empty(nbytes + 256, dtype=torch.uint8, device=dev)
+        off = (-sh.data_ptr()) % 256
+        sh = sh[off:off + nbytes]
+        _SHADOW[key] = sh
+    return sh
+
+
+def release_buffers() -> None:
+    """Drops the cached workspaces and cache shadows (they are re-created on the next launch)."""
+    _WS.clear()
+    _SHADOW.clear()
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def check_shapes(w1, wo, w2, w3, scales, mods, mod_final, rope_cos, rope_sin, w_ain, b_ain, w_aout, b_aout,
+                 kvsrc_k, kvsrc_v, srows, kcache, vtcache, Lp, Lmax, num_steps, Tv, x_t, nl, batch):
+    """Every size the kernels address, checked on the host (src/pi05/binding.cpp:38-56 takes the
+    same tensors unchecked; the kernels here would read or write out of range on a mismatch)."""
+    _need(nl >= 1 and num_steps >= 1, f"need num_layers >= 1 and num_steps >= 1 (got {nl}, {num_steps})")
+    _need(1 <= Tv <= MAX_TV, f"Tv={Tv} outside [1, {MAX_TV}]")
+    _need(Lp >= 0 and Lmax >= Lp + Tv and Lmax % 16 == 0, f"Lmax={Lmax} must be a multiple of 16 and >= Lp+Tv={Lp + Tv}")
+    for name, t, per in (("w1", w1, 2560 * D), ("wo", wo, D * QD), ("w2", w2, 2 * F * D), ("w3", w3, D * F)):
+        _need(t.numel() >= nl * per and t.numel() % per == 0, f"{name} holds {t.numel()} elements, not [>= {nl}][{per}]")
+    if scales is not None:
+        for name, t, per in zip(("s1", "so", "s2", "s3"), scales, (2560, D, 2 * F, D)):
+            _need(t.numel() >= nl * per, f"{name} holds {t.numel()} row scales, need {nl} x {per}")
+    _need(mods.numel() >= num_steps * nl * 2 * 3 * D, f"mods holds {mods.numel()} values, need [{num_steps}][{nl}][2][3072]")
+    _need(mod_final.numel() >= num_steps * 3 * D, f"mod_final holds {mod_final.numel()} values, need [{num_steps}][3072]")
+    for name, t in (("rope_cos", rope_cos), ("rope_sin", rope_sin)):
+        _need(t.dim() == 2 and t.shape[1] == HD // 2 and t.shape[0] >= Tv,
+              f"{name} must be [>= Tv={Tv}][128], got {tuple(t.shape)}")
+    for name, t, n in (("w_ain", w_ain, D * AD), ("b_ain", b_ain, D), ("w_aout", w_aout, AD * D), ("b_aout", b_aout, AD)):
+        _need(t.numel() == n, f"{name} holds {t.numel()} values, need {n}")
+    _need(x_t.shape[-1] == AD and x_t.dim() in (2, 3) and x_t.shape[-2] >= Tv,
+          f"x_t must be [batch][rows >= Tv][32] or [rows][32], got {tuple(x_t.shape)}")
+    per = nl * Lmax * HD
+    for name, t in (("kcache", kcache), ("vtcache", vtcache)):
+        ok = t.numel() == batch * per if batch > 1 else t.numel() >= per and t.numel() % (Lmax * HD) == 0
+        _need(ok, f"{name} holds {t.numel()} elements, need [batch={batch}][NL={nl}][{Lmax}][{HD}]")
+    _need(kcache.shape[-1] == HD and kcache.shape[-2] == Lmax, f"kcache must end in [Lmax={Lmax}][256], got {tuple(kcache.shape)}")
+    _need(vtcache.shape[-1] == Lmax and vtcache.shape[-2] == HD, f"vtcache must end in [256][Lmax={Lmax}], got {tuple(vtcache.shape)}")
+    if srows > 0:
+        for name, t in (("kvsrc_k", kvsrc_k), ("kvsrc_v", kvsrc_v)):
+            _need(t is not None and t.numel() >= batch * nl * srows * HD and t.dtype == torch.bfloat16,
+                  f"{name} must be bf16 [batch][NL][srows={srows}][256]")
+        _need(srows >= Lp, f"srows={srows} < Lp={Lp}")
+
+
 def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
            w_ain, b_ain, w_aout, b_aout, kvsrc_k, kvsrc_v, srows,
            kcache, vtcache, Lp, Lmax, num_steps, Tv,
            x_t, x=None, xp=None, stage_cycles=None, xn=None, q=None, attn=None, hmlp=None, scores=None,
            probs=None, nblocks=None, nthreads=None, *, num_layers=None, workspace_tensor=None, trace=None,
-           trace_layer=0):
+           trace_layer=0, check_status=False):
     """Runs the whole ``num_steps`` Euler loop; ``x_t`` is updated in place (the output).
 
     Same positional order as the reference ``launch``. Differences, all by design:
       * weights are bf16 ([NL][2560][1024] ... as packed by ``pack_weights``) with s1..s3 empty/None,
         or FP8-W8A16 (batch 1): e4m3 codes (uint8 or float8_e4m3fn) with fp32 per-row scales s1..s3,
         as ``pack_weights_fp8`` makes them (the reference's quantisation);
-      * kcache/vtcache are bf16 (the reference used fp16);
+      * kcache/vtcache are bf16, or fp16 as the reference allocates them: the C ABI then runs on a
+        bf16 shadow (``cache_shadow()``) and writes the rows it produced back in fp16;
       * the scratch tensors x, xp, xn, q, attn, hmlp, scores, probs are accepted and ignored: the
         MI355X engine keeps its intermediates in one workspace (``workspace()``);
-      * nblocks/nthreads are ignored: the grid is one 256-thread workgroup per CU (256);
-      * stage_cycles (int64, >= 16 entries) receives 100 MHz real-time ticks per stage.
+      * nblocks/nthreads are ignored: the grid is one workgroup per CU (256);
+      * stage_cycles (int64, >= 16 entries) accumulates ticks of the 100 MHz GPU clock per stage
+        (``_lib.STAGE_TICK_HZ``), where the reference accumulates clock64() cycles;
+      * check_status=True waits for the launch, reads the kernel status and, when it is non-zero
+        (a capped wait expired, or the XCD placement differed), re-initialises the workspace and
+        raises FlashActError.
     Rows [Tv, rows) of x_t are left untouched (the reference also integrates padded rows).
     """
     L = _lib.lib()
@@ -216,19 +285,23 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
     for name, t in (("wo", wo), ("w2", w2), ("w3", w3)):
         if t.dtype != w1.dtype:
             raise TypeError(f"{name} dtype {t.dtype} differs from w1 {w1.dtype}")
-    if kcache.dtype != torch.bfloat16 or vtcache.dtype != torch.bfloat16:
-        raise TypeError("kcache and vtcache must be bfloat16")
+    if kcache.dtype != vtcache.dtype or kcache.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"kcache and vtcache must both be bfloat16 or both float16, got {kcache.dtype}, {vtcache.dtype}")
     for name, t in (("mods", mods), ("mod_final", mod_final), ("rope_cos", rope_cos), ("rope_sin", rope_sin),
                     ("w_ain", w_ain), ("b_ain", b_ain), ("w_aout", w_aout), ("b_aout", b_aout), ("x_t", x_t)):
         if t.dtype != torch.float32:
             raise TypeError(f"{name} must be float32, got {t.dtype}")
     nl = int(num_layers) if num_layers is not None else int(w1.shape[0])
-    batch = 1
+    batch = int(x_t.shape[0]) if x_t.dim() == 3 else 1
     xt_rows = int(x_t.shape[-2])
-    if x_t.dim() == 3:
-        batch = int(x_t.shape[0])
+    Lp, Lmax, num_steps, Tv, srows = int(Lp), int(Lmax), int(num_steps), int(Tv), int(srows)
+    check_shapes(w1, wo, w2, w3, (s1, so_, s2, s3) if wdt == _lib.FA_DTYPE_FP8_E4M3 else None, mods, mod_final,
+                 rope_cos, rope_sin, w_ain, b_ain, w_aout, b_aout, kvsrc_k, kvsrc_v, srows, kcache, vtcache, Lp,
+                 Lmax, num_steps, Tv, x_t, nl, batch)
+    if not x_t.is_cuda:
+        raise ValueError("all tensors must be on the GPU (x_t is not)")
     dev = x_t.device
-    ws = workspace_tensor if workspace_tensor is not None else workspace(dev, batch, int(Tv), int(Lmax))
+    ws = workspace_tensor if workspace_tensor is not None else workspace(dev, batch, Tv, Lmax)
     a = _lib.Pi05Args()
     a.weight_dtype = wdt
     a.w1, a.wo, a.w2, a.w3 = _ptr(w1), _ptr(wo), _ptr(w2), _ptr(w3)
@@ -236,9 +309,9 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
     a.mods, a.mod_final = _ptr(mods), _ptr(mod_final)
     a.rope_cos, a.rope_sin = _ptr(rope_cos), _ptr(rope_sin)
     a.w_ain, a.b_ain, a.w_aout, a.b_aout = _ptr(w_ain), _ptr(b_ain), _ptr(w_aout), _ptr(b_aout)
-    a.kvsrc_k, a.kvsrc_v, a.srows = _ptr(kvsrc_k), _ptr(kvsrc_v), int(srows)
+    a.kvsrc_k, a.kvsrc_v, a.srows = _ptr(kvsrc_k) if srows > 0 else None, _ptr(kvsrc_v) if srows > 0 else None, srows
     a.kcache, a.vtcache = _ptr(kcache), _ptr(vtcache)
-    a.Lp, a.Lmax, a.num_steps, a.Tv = int(Lp), int(Lmax), int(num_steps), int(Tv)
+    a.Lp, a.Lmax, a.num_steps, a.Tv = Lp, Lmax, num_steps, Tv
     a.num_layers, a.batch = nl, batch
     a.x_t, a.xt_rows = _ptr(x_t), xt_rows
     if stage_cycles is not None and stage_cycles.numel() > 0:
@@ -250,5 +323,21 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
         if trace.dtype != torch.int64 or trace.numel() < 256 * 6 * 32:
             raise TypeError("trace must be an int64 tensor with >= 256*6*32 entries")
         a.trace, a.trace_layer = _ptr(trace), int(trace_layer)
-    stream = torch.cuda.current_stream(dev).cuda_stream
-    _lib.check(L.fa_pi05_denoise(ctypes.byref(a), ctypes.c_void_p(stream)), "fa_pi05_denoise")
+    if kcache.dtype == torch.float16:
+        sh = cache_shadow(dev, batch, nl, Lmax)
+        a.cache_dtype, a.cache_shadow, a.cache_shadow_bytes = _lib.FA_DTYPE_F16, sh.data_ptr(), sh.numel()
+    stream = torch.cuda.current_stream(dev)
+    _lib.check(L.fa_pi05_denoise(ctypes.byref(a), ctypes.c_void_p(stream.cuda_stream)), "fa_pi05_denoise")
+    if check_status:
+        raise_on_status(ws, stream)
+
+
+def raise_on_status(ws: torch.Tensor, stream=None) -> None:
+    """Waits for `stream`, reads the kernel status of the workspace's last launch; a non-zero status
+    re-initialises the workspace (its control words are then undefined) and raises FlashActError."""
+    (stream or torch.cuda.current_stream(ws.device)).synchronize()
+    st = read_status(ws)
+    if st != 0:
+        reset_workspace(ws)
+        raise _lib.FlashActError(f"fa_pi05_denoise kernel status {st:#x} (1 = capped wait expired, 2 = XCD placement "
+                                 "differed): the chunk is invalid; the workspace was re-initialised")

@@ -177,7 +177,9 @@ class Pi05Policy:
         p = self.packed
         empty = torch.empty(0, device=dev)
         sc = [p.get(k, empty) for k in ("s1", "so", "s2", "s3")]
+        # check_status: waits for the chunk and raises (after re-initialising the workspace) if a
+        # capped wait expired or the XCD placement differed, so an invalid chunk is never returned
         pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], *sc, self.mods, self.mod_final,
                     cos, sin, self.w_ain, self.b_ain, self.w_aout, self.b_aout, ksrc, vsrc, srows, kc, vc, Lp, Lmax,
-                    self.num_steps, self.chunk_size, x_t)
+                    self.num_steps, self.chunk_size, x_t, check_status=True)
         return x_t.cpu().numpy()

@@ -61,6 +61,11 @@ def read_status(ws: torch.Tensor) -> int:
     return pi05.read_status(ws)
 
 
+def release_buffers() -> None:
+    """Drops the cached workspaces (they are re-created on the next launch)."""
+    _WS.clear()
+
+
 def _ptr(t, name):
     if not isinstance(t, torch.Tensor) or not t.is_cuda:
         raise ValueError(f"{name} must be a GPU tensor")

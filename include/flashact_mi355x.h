@@ -31,7 +31,12 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
+
+/* Unit of every stage_cycles counter: ticks of the GPU's constant 100 MHz real-time clock
+ * (s_memrealtime), accumulated (+=) into the caller's counters like the reference's clock64()
+ * cycles (src/pi05/mk6.cu:129-134); the caller zeroes them. microseconds = ticks / 100. */
+#define FA_STAGE_TICK_HZ 100000000
 
 struct ihipStream_t;
 typedef struct ihipStream_t* fa_stream_t; /* identical to hipStream_t */
@@ -44,7 +49,7 @@ enum fa_status {
   FA_ERR_LAUNCH = 4        /* the HIP launch itself failed */
 };
 
-enum fa_dtype { FA_DTYPE_BF16 = 0, FA_DTYPE_FP8_E4M3 = 1 };
+enum fa_dtype { FA_DTYPE_BF16 = 0, FA_DTYPE_FP8_E4M3 = 1, FA_DTYPE_F16 = 2 };
 
 /* Kernel-side status bits (read back from the workspace by fa_*_read_status). */
 #define FA_KSTATUS_SPIN_TIMEOUT 1u /* a grid/XCD barrier wait hit its cap: results invalid */
@@ -55,7 +60,8 @@ typedef struct fa_device_info {
   int xcds;              /* accelerator complex dies */
   int lds_bytes;         /* LDS per workgroup */
   int coop_launch;       /* cooperative launch supported */
-  int coop_max_blocks;   /* max co-resident workgroups of the pi0.5 kernel */
+  int coop_max_blocks;   /* co-resident workgroups of the batch-1 pi0.5 kernel (occupancy x CUs;
+                          * 0 if that kernel cannot run on the device) */
   char arch[64];         /* gcnArchName */
 } fa_device_info;
 
@@ -67,8 +73,10 @@ typedef struct fa_device_info {
  *   wo [NL][1024][2048]; w2 [NL][8192][1024]: rows 2f = gate f, 2f+1 = up f; w3 [NL][1024][4096].
  * mods [S][NL][2][3072] (scale | shift | gate, for input/post-attention norms), mod_final [S][3072].
  * rope_cos/sin [Tv][128] for positions Lp + t. w_ain [1024][32], b_ain [1024], w_aout [32][1024],
- * b_aout [32] (fp32). kcache bf16 [batch][NL][Lmax][256] holds RoPE'd prefix keys in rows [0, Lp);
- * vtcache bf16 [batch][NL][256][Lmax] holds the transposed prefix values in columns [0, Lp).
+ * b_aout [32] (fp32). kcache [batch][NL][Lmax][256] holds RoPE'd prefix keys in rows [0, Lp);
+ * vtcache [batch][NL][256][Lmax] holds the transposed prefix values in columns [0, Lp). The caches
+ * are bf16, or fp16 as the reference allocates them (benchmarks/pi05/eval_numerics.py:83-85,
+ * src/pi05/hybrid_model.py:172-173): see cache_dtype.
  * The launch writes the suffix rows/columns [Lp, Lp+Tv) of both caches (as the reference does)
  * and updates x_t in place: x_t [batch][xt_rows][32] fp32, rows [0, Tv) of each sample.
  */
@@ -110,7 +118,7 @@ typedef struct fa_pi05_args {
   int batch;      /* 1 (batched launches: see fa_pi05_max_batch) */
   float* x_t;
   int xt_rows;
-  unsigned long long* stage_cycles; /* optional [16]: per-stage 100 MHz ticks, workgroup 0 */
+  unsigned long long* stage_cycles; /* optional [16]: per-stage ticks (FA_STAGE_TICK_HZ), workgroup 0, += */
   void* workspace;
   size_t workspace_bytes;
   /* Diagnostics (optional): for global layer index trace_layer (= step * num_layers + layer),
@@ -119,11 +127,23 @@ typedef struct fa_pi05_args {
    * layer's weight pages was issued and landed: trace [256 workgroups][6][32]. NULL disables. */
   unsigned long long* trace;
   int trace_layer;
+  /* Cache element type: FA_DTYPE_BF16 (0), or FA_DTYPE_F16 for the reference's fp16 caches. With
+   * fp16 caches the launch converts both caches to bf16 into cache_shadow (at least
+   * fa_pi05_cache_shadow_bytes(batch, num_layers, Lmax) bytes, 256-byte aligned, caller-owned),
+   * runs the loop on the shadow (the hand-off, srows > 0, writes it too) and converts the rows it
+   * wrote back into the caller's fp16 caches: [Lp, Lp+Tv), and [0, Lp) as well with srows > 0.
+   * fp16 -> bf16 rounds each cached value to 8 significant bits, as the bf16 operands of the
+   * attention MFMAs would. cache_shadow is ignored for bf16 caches. */
+  int cache_dtype;
+  void* cache_shadow;
+  size_t cache_shadow_bytes;
 } fa_pi05_args;
 
 /* Whole S-step Euler loop as ONE cooperative launch (256 workgroups, one per CU). */
 int fa_pi05_denoise(const fa_pi05_args* args, fa_stream_t stream);
 size_t fa_pi05_workspace_bytes(int batch, int Tv, int Lmax);
+/* Bytes of the bf16 cache shadow an fp16-cache launch needs (see cache_dtype). */
+size_t fa_pi05_cache_shadow_bytes(int batch, int num_layers, int Lmax);
 /* Zeroes a workspace (required once after allocation and after a non-zero kernel status). */
 int fa_pi05_workspace_init(void* workspace, size_t bytes, fa_stream_t stream);
 /* Synchronous: copies the kernel status bits (FA_KSTATUS_*) of the last launch on this workspace. */
@@ -180,7 +200,7 @@ typedef struct fa_ma2_args {
   int batch;
   float* x_t;
   int xt_rows;
-  unsigned long long* stage_cycles; /* optional [16]: per-stage 100 MHz ticks, workgroup 0 */
+  unsigned long long* stage_cycles; /* optional [16]: per-stage ticks (FA_STAGE_TICK_HZ), workgroup 0, += */
   void* workspace;
   size_t workspace_bytes;
 } fa_ma2_args;
@@ -227,7 +247,7 @@ typedef struct fa_prefill_args {
   int Lmax;
   int num_layers;
   int batch;
-  unsigned long long* stage_cycles; /* optional [16]: per-stage 100 MHz ticks, workgroup 0 */
+  unsigned long long* stage_cycles; /* optional [16]: per-stage ticks (FA_STAGE_TICK_HZ), workgroup 0, += */
   void* workspace;
   size_t workspace_bytes;
 } fa_prefill_args;

@@ -38,6 +38,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#include <immintrin.h>
 #ifdef _OPENMP
 #include <omp.h>
 #endif
@@ -68,17 +69,53 @@ int fo_num_threads(void) {
 #endif
 }
 
-/* Y[m][n] = sum_k X[m][k] * W[n][k] (+ bias[n]); W bf16 [N][K]. */
+/* The 2 x 4 dot products of rows x0, x1 with rows w[0..3] (stride K), K a multiple of 8. Each keeps
+ * dot_f32's eight partial sums and their reduction order, so every result equals dot_f32's; the
+ * blocking only lets one load of x serve four weight rows. */
+static inline void dot_2x4(const float* x0, const float* x1, const float* w, int K, float r[2][4]) {
+  __m256 s[2][4];
+  for (int b = 0; b < 4; b++) s[0][b] = s[1][b] = _mm256_setzero_ps();
+  for (int i = 0; i < K; i += 8) {
+    const __m256 a0 = _mm256_loadu_ps(x0 + i), a1 = _mm256_loadu_ps(x1 + i);
+    for (int b = 0; b < 4; b++) {
+      const __m256 wv = _mm256_loadu_ps(w + (size_t)b * K + i);
+      s[0][b] = _mm256_fmadd_ps(a0, wv, s[0][b]);
+      s[1][b] = _mm256_fmadd_ps(a1, wv, s[1][b]);
+    }
+  }
+  for (int a = 0; a < 2; a++)
+    for (int b = 0; b < 4; b++) {
+      float t[8];
+      _mm256_storeu_ps(t, s[a][b]);
+      r[a][b] = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+    }
+}
+
+/* Y[m][n] = sum_k X[m][k] * W[n][k] (+ bias[n]); W bf16 [N][K]. Weight rows are converted to fp32 in
+ * blocks of four and each pair of X rows is multiplied with the block (dot_2x4). */
 static void linear_bf16(const float* X, int M, int K, const uint16_t* W, const float* bias, int N, float* Y) {
 #pragma omp parallel
   {
-    float* wrow = (float*)malloc(sizeof(float) * (size_t)K);
+    float* wrow = (float*)malloc(sizeof(float) * 4 * (size_t)K);
 #pragma omp for schedule(static)
-    for (int n = 0; n < N; n++) {
-      const uint16_t* w = W + (size_t)n * K;
-      for (int k = 0; k < K; k++) wrow[k] = bf(w[k]);
-      float b = bias ? bias[n] : 0.f;
-      for (int m = 0; m < M; m++) Y[(size_t)m * N + n] = dot_f32(X + (size_t)m * K, wrow, K) + b;
+    for (int n0 = 0; n0 < N; n0 += 4) {
+      const int nb = N - n0 < 4 ? N - n0 : 4;
+      for (int j = 0; j < nb; j++) {
+        const uint16_t* w = W + (size_t)(n0 + j) * K;
+        for (int k = 0; k < K; k++) wrow[(size_t)j * K + k] = bf(w[k]);
+      }
+      int m = 0;
+      if (nb == 4 && K % 8 == 0) {
+        for (; m + 2 <= M; m += 2) {
+          float r[2][4];
+          dot_2x4(X + (size_t)m * K, X + (size_t)(m + 1) * K, wrow, K, r);
+          for (int a = 0; a < 2; a++)
+            for (int j = 0; j < 4; j++) Y[(size_t)(m + a) * N + n0 + j] = r[a][j] + (bias ? bias[n0 + j] : 0.f);
+        }
+      }
+      for (; m < M; m++)
+        for (int j = 0; j < nb; j++)
+          Y[(size_t)m * N + n0 + j] = dot_f32(X + (size_t)m * K, wrow + (size_t)j * K, K) + (bias ? bias[n0 + j] : 0.f);
     }
     free(wrow);
   }

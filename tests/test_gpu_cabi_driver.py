@@ -1,0 +1,94 @@
+"""C++ host code calling the engine through its C ABI alone (tests/cabi_driver.cpp, built by
+``flashact_amd.build``): no Python binding and no torch between the caller and the kernels.
+
+The test writes a seeded case as raw files, runs the driver as a child process, and compares the
+x_t it writes back with the CPU oracle at the BASELINE tolerance (max-abs <= 2e-2, mean-abs <= 2e-3);
+for pi0.5 it also checks the suffix cache rows against a launch of the same case through ctypes.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from flashact_amd import ma2, pi05
+from flashact_amd.build import DRIVER_PATH
+from tests import ma2_case as M
+from tests import pi05_case as P
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+pytestmark = pytest.mark.gpu
+
+
+def _write(d, name, t):
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        t = t.view(torch.int16)
+    t.numpy().tofile(os.path.join(d, name + ".bin"))
+
+
+def _run(args):
+    if not os.path.exists(DRIVER_PATH):
+        pytest.fail(f"{DRIVER_PATH} is missing: run __graft_entry__.build() first")
+    print("cabi_driver", " ".join(str(a) for a in args), flush=True)
+    res = subprocess.run([DRIVER_PATH, *map(str, args)], capture_output=True, text=True, timeout=120)
+    print(res.stdout.strip(), res.stderr.strip(), flush=True)
+    assert res.returncode == 0, res.stderr
+    return res.stdout
+
+
+def test_cpp_driver_pi05(gpu, tmp_path):
+    NL, Lp, Tv, S, rows = 2, 300, 50, 2, 56
+    c = P.make_case(NL=NL, Lp=Lp, Tv=Tv, S=S, seed=31)
+    g = P.gpu_tensors(c, "cpu")
+    d = str(tmp_path)
+    for k in ("w1", "wo", "w2", "w3"):
+        _write(d, k, g["packed"][k])
+    kc, vc = g["caches"][0]
+    x_t = torch.zeros(rows, 32)
+    x_t[:Tv] = c["inp"]["noise"][0]
+    for k, t in (("mods", g["mods"]), ("mod_final", g["mod_final"]), ("rope_cos", g["cos"]), ("rope_sin", g["sin"]),
+                 ("w_ain", g["w_ain"]), ("b_ain", g["b_ain"]), ("w_aout", g["w_aout"]), ("b_aout", g["b_aout"]),
+                 ("kcache", kc), ("vtcache", vc), ("x_t", x_t)):
+        _write(d, k, t)
+    out = _run(["pi05", d, NL, Lp, Tv, S, g["Lmax"], rows])
+    assert "cus=256" in out and "coop_max_blocks=256" in out
+    xo = np.fromfile(os.path.join(d, "x_t.out"), dtype=np.float32).reshape(rows, 32)
+    ref = P.run_oracle(c)[0]
+    st = P.parity(xo[:Tv], ref)
+    print(f"C++ driver pi05 NL={NL} Lp={Lp} Tv={Tv} S={S}: {st}", flush=True)
+    assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
+    assert np.all(xo[Tv:] == 0.0)
+    # the same case through the Python binding: identical actions and suffix cache rows
+    xg, kg, vg = P.run_gpu(c, gpu, xt_rows=rows)
+    assert np.array_equal(xg, xo)
+    ko = np.fromfile(os.path.join(d, "kcache.out"), dtype=np.uint16).reshape(NL, g["Lmax"], 256)
+    vo = np.fromfile(os.path.join(d, "vtcache.out"), dtype=np.uint16).reshape(NL, 256, g["Lmax"])
+    assert np.array_equal(ko, P.u16(kg)) and np.array_equal(vo, P.u16(vg))
+
+
+def test_cpp_driver_ma2(gpu, tmp_path):
+    NL, Lk, Tv, S, adim, rows = 2, 493, 30, 2, 6, 32
+    c = M.make_case(NL=NL, Lk=Lk, Tv=Tv, S=S, adim=adim, seed=32)
+    g = M.gpu_tensors(c, "cpu")
+    d = str(tmp_path)
+    for k, t in zip(("w_qkv", "w_so", "w_cq", "w_co", "w_gu", "w_dn"), g["ws"]):
+        _write(d, k, t)
+    for k, t in zip(("b_qkv", "b_so", "b_cq", "b_co", "b_gu", "b_dn"), g["bs"]):
+        _write(d, k, t)
+    x_t = torch.zeros(rows, 32)
+    x_t[:Tv] = c["inp"]["noise"][0]
+    for k, t in (("mods", g["mods"]), ("mod_final", g["mod_final"]), ("rope_cos", g["cos"]), ("rope_sin", g["sin"]),
+                 ("w_ain", g["w_ain"]), ("b_ain", g["b_ain"]), ("w_aout", g["w_aout"]), ("b_aout", g["b_aout"]),
+                 ("kctx", g["kc"][0]), ("vtctx", g["vt"][0]), ("x_t", x_t)):
+        _write(d, k, t)
+    _run(["ma2", d, NL, Lk, g["Lkmax"], Tv, adim, S, rows])
+    xo = np.fromfile(os.path.join(d, "x_t.out"), dtype=np.float32).reshape(rows, 32)
+    ref = M.run_oracle(c)[0]
+    st = M.parity(xo[:Tv], ref, adim)
+    print(f"C++ driver ma2 NL={NL} Lk={Lk} Tv={Tv} S={S}: {st}", flush=True)
+    assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
+    assert np.all(xo[Tv:] == 0.0)
+    assert np.array_equal(xo[:Tv, adim:], c["inp"]["noise"][0, :, adim:].numpy())

@@ -45,7 +45,14 @@ def test_ma2_edge_shapes(gpu, B, Lk, Tv, S, adim):
 
 
 def test_ma2_batch16(gpu):
-    """BASELINE config 4 at batch 16 (the large-tile path), 2 layers and 2 steps against the oracle."""
+    """BASELINE config 4 at batch 16 (the large-tile path) at full depth, 36 layers x 10 steps, every
+    sample against the oracle (benchmarks/molmoact2/eval_numerics.py:147-159 is the reference's
+    fidelity check of the same loop)."""
+    _check(C.make_case(NL=36, Lk=493, Tv=30, S=10, batch=16), gpu)
+
+
+def test_ma2_batch16_shallow(gpu):
+    """Batch 16 at 2 layers and 2 steps: a quick first signal before the full-depth case."""
     _check(C.make_case(NL=2, Lk=493, Tv=30, S=2, batch=16), gpu)
 
 

@@ -51,17 +51,47 @@ def test_prefill_edge_shapes(gpu, Lp, B):
     _check_kv(c, kc, vt)
 
 
-def test_prefill_config3_shape_first_layers(gpu):
-    """The full BASELINE config 3 launch (18 layers, Lp = 968): layers 0-1 against the oracle (the
-    first layers' K/V do not depend on the layer count), every layer finite and non-trivial."""
-    c = C.make_case(NL=18, Lp=968, device=gpu)
-    kc, vt = C.run_gpu(c, gpu, Lmax=pi05.lmax_for(968, 50))
-    c2 = dict(c, NL=2, w={k: v[:2] for k, v in c["w"].items()})
-    K, V = C.run_oracle(c2)
-    _check_kv(c2, kc[:, :2].contiguous(), vt[:, :2].contiguous(), K, V)
-    k = kc[:, :, :968].float()
-    assert torch.isfinite(k).all() and torch.isfinite(vt.float()).all()
-    assert (k.abs().amax(dim=(0, 2, 3)) > 0.1).all()  # every layer wrote its keys
+@pytest.fixture(scope="module")
+def config3(gpu):
+    """BASELINE config 3's prefill (18 layers, Lp = 968) on the GPU and in the oracle, shared by the
+    full-depth K/V check and the full chain below (the oracle prefill is the slow part)."""
+    c = C.make_case(NL=18, Lp=968)
+    Lmax = pi05.lmax_for(968, 50)
+    kc, vt = C.run_gpu(c, gpu, Lmax=Lmax)
+    ws = prefill.workspace(gpu, 1, 968, Lmax)
+    assert prefill.read_status(ws) == 0
+    K, V = C.run_oracle(c)
+    return c, kc, vt, K, V, Lmax
+
+
+def test_prefill_config3_all_layers(config3):
+    """The full BASELINE config 3 launch: K/V of every one of the 18 layers against the oracle."""
+    c, kc, vt, K, V, _ = config3
+    for l in range(c["NL"]):
+        st = C.kv_diff(kc[:, l:l + 1], vt[:, l:l + 1], K[:, l:l + 1], V[:, l:l + 1], c["Lp"])
+        print(f"config 3 prefill layer {l}: {st}", flush=True)
+        assert st["k_max"] <= KV_MAX and st["v_max"] <= KV_MAX, (l, st)
+        assert st["k_mean"] <= KV_MEAN and st["v_mean"] <= KV_MEAN, (l, st)
+
+
+def test_config3_full_chain(gpu, config3):
+    """BASELINE config 3 end to end at full size: the 18-layer prefill over 968 tokens writes the
+    caches, the 18-layer, 10-step, Tv = 50 denoise loop reads them; final actions against the oracle
+    chain (oracle prefill -> bf16 K/V -> oracle denoise), as eval_numerics.py:50-69 and :81-107 chain
+    openpi's prefill, the cache fill and the loop."""
+    pc, kc, vt, K, V, Lmax = config3
+    Tv = 50
+    dc = P.make_case(NL=18, Lp=968, Tv=Tv, S=10, seed=41)
+    dc["inp"]["kpre"] = torch.from_numpy(K).to(torch.bfloat16)
+    dc["inp"]["vpre"] = torch.from_numpy(V).to(torch.bfloat16)
+    ref = P.run_oracle(dc)[0]
+    g = P.gpu_tensors(dc, gpu)
+    assert g["Lmax"] == Lmax
+    g["caches"] = [(kc[0].clone(), vt[0].clone())]
+    out = P.run_gpu(dc, gpu, g)[0]
+    st = P.parity(out[:Tv], ref)
+    print(f"config 3 full chain (18-layer prefill Lp=968 -> 18 layers x 10 steps, Tv={Tv}): {st}", flush=True)
+    assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
 
 
 def test_prefill_batch_matches_single(gpu):

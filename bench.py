@@ -53,6 +53,11 @@ MA2_STAGES = {0: "N_msa", 1: "QKV", 2: "SATT", 3: "SO", 4: "N_mca", 5: "CQ", 6: 
 PREFILL_STAGES = {0: "N1", 1: "QKV", 2: "ATT", 3: "COMB", 4: "O", 5: "N2", 6: "GU", 7: "DN", 9: "grid_barriers"}
 
 
+def log(msg: str) -> None:
+    """Progress line on stderr (the JSON result is the only stdout line)."""
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
 def parity(out, ref) -> dict:
     a, b = np.asarray(out, np.float64).ravel(), np.asarray(ref, np.float64).ravel()
     d = np.abs(a - b)
@@ -416,6 +421,7 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    log("building the BASELINE config 1 inputs")
     w, inp, mods, modf, packed, cos, sin, Lmax, kc, vc = build_inputs(dev)
     x_t = inp["noise"][0].clone()
     empty = torch.empty(0, device=dev)
@@ -474,9 +480,12 @@ def main():
         "kernel_status": status,
         "stage_us_per_layer": stage_us(dev, step, PI05_BS1_STAGES, NL * S),
     }
+    log(f"config 1: {ms_per_step:.3f} ms per chunk")
     if args.bs16_launches > 0:
+        log("config 2 (batch 16)")
         res["bs16"] = bench_batched(dev, 16, args.bs16_launches, 2, check=not args.no_cpu)
     if args.ref_shape_launches > 0:
+        log("reference shape (Tv = 10)")
         # The reference's published loop number (9.5 ms, src/pi05/README.md:19) is for horizon 10
         # (T = 16 padded) over a LIBERO prefix, fp8 weights, on an RTX 5090: the same kernel at Tv = 10.
         tv10 = 10
@@ -503,6 +512,7 @@ def main():
                                   "reference_published_setup": "RTX 5090, fp8 weights, horizon 10 (T=16), LIBERO "
                                                                "prefix, 10 steps (src/pi05/README.md:19)"}
     if args.fp8_launches > 0:
+        log("fp8 weights")
         # FP8-W8A16 weights (the reference's pi0.5 numerics): BASELINE shape and the reference's Tv = 10.
         pk8 = pi05.pack_weights_fp8(w["wq"], w["wk"], w["wv"], w["wo"], w["wg"], w["wu"], w["wd"])
         fp8 = {"workload": "pi05_expert_bs1_T50_Lp968_S10 with FP8-W8A16 weights (per-row e4m3)"}
@@ -535,6 +545,7 @@ def main():
         res["fp8"] = fp8
         del pk8
     if args.prefill_launches > 0:
+        log("config 3 (prefill + denoise)")
         kc3, vc3 = torch.zeros_like(kc), torch.zeros_like(vc)
         x3 = inp["noise"][0].clone()
 
@@ -554,9 +565,11 @@ def main():
         res["config3"] = bench_prefill(dev, args.prefill_launches, step3, kc3, vc3, check=check)
         del kc3, vc3
     if args.ma2_launches > 0:
+        log("config 4 (MolmoAct2 batch 1 and 16)")
         res["molmoact2"] = {"bs1": bench_ma2(dev, 1, args.ma2_launches, cpu=not args.no_cpu),
                             "bs16": bench_ma2(dev, 16, args.ma2_launches, cpu=not args.no_cpu)}
     if not args.no_cpu:
+        log("cpu_baseline (oracle, 1 warmup + 3 timed chunks)")
         cpu_ms, cpu_runs, ref, threads = cpu_baseline(w, inp, mods, modf, cos, sin)
         res["cpu_baseline"] = {"value": round(cpu_ms, 1), "unit": "ms per chunk", "cores": threads, "kind": "port",
                                "sample": "one full chunk (18 layers x 10 Euler steps, Lp=968, Tv=50) of the fp32 "

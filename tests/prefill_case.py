@@ -55,3 +55,59 @@ def kv_diff(kc, vt, K, V, Lp):
     dk, dv = np.abs(kg - K), np.abs(vg - V)
     return {"k_max": float(dk.max()), "k_mean": float(dk.mean()), "v_max": float(dv.max()),
             "v_mean": float(dv.mean()), "ref_max": float(max(np.abs(K).max(), np.abs(V).max()))}
+
+
+def run_bf16_floor(c):
+    """(K, V) [batch][NL][Lp][256] of a torch restatement of the prefill in fp32 arithmetic whose
+    matmul operands are rounded to bf16 where bf16 MFMAs take them: the normed rows, q, k, v, the
+    softmax weights of each 128-key chunk and that chunk's normalised output, the combined attention
+    output and the MLP activation. Its distance to the fp32 oracle is the error that bf16 operands
+    alone produce (the floor a bf16 kernel is held to); it is not the oracle."""
+    w = c["w"]
+    bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+    cos, sin = c["cos"].float(), c["sin"].float()
+
+    def rms(x, ln):
+        return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-6) * (1 + ln)
+
+    def rope(v):
+        a, b = v[..., :128], v[..., 128:]
+        cc, ss = (cos[:, None], sin[:, None]) if v.dim() == 3 else (cos, sin)
+        return torch.cat([a * cc - b * ss, b * cc + a * ss], -1)
+
+    NL, Lp = c["NL"], c["Lp"]
+    Ks, Vs = [], []
+    for b in range(c["batch"]):
+        x = c["x"][b].float().cpu().clone()
+        kl, vl = [], []
+        for l in range(NL):
+            h = bf(rms(x, w["ln_in"][l].float().cpu()))
+            q = bf(rope((h @ w["wq"][l].float().cpu().T).view(Lp, 8, 256)))
+            k = bf(rope(h @ w["wk"][l].float().cpu().T))
+            v = bf(h @ w["wv"][l].float().cpu().T)
+            kl.append(k)
+            vl.append(v)
+            if l == NL - 1:
+                break
+            s = torch.einsum("thd,jd->htj", q, k) / 16.0
+            outs, ms, ls = [], [], []
+            for c0 in range(0, Lp, 128):
+                sc = s[:, :, c0:c0 + 128]
+                m = sc.amax(-1, keepdim=True)
+                p = torch.exp(sc - m)
+                lsum = p.sum(-1, keepdim=True)
+                outs.append(bf((bf(p) @ v[c0:c0 + 128]) / lsum))
+                ms.append(m)
+                ls.append(lsum)
+            M = torch.stack(ms).amax(0)
+            wsum = sum(l_ * torch.exp(m_ - M) for l_, m_ in zip(ls, ms))
+            att = sum(o * l_ * torch.exp(m_ - M) for o, l_, m_ in zip(outs, ls, ms)) / wsum
+            att = bf(att).permute(1, 0, 2).reshape(Lp, 8 * 256)
+            x = x + att @ w["wo"][l].float().cpu().T
+            h = bf(rms(x, w["ln_post"][l].float().cpu()))
+            g = h @ w["wg"][l].float().cpu().T
+            u = h @ w["wu"][l].float().cpu().T
+            x = x + bf(torch.nn.functional.gelu(g, approximate="tanh") * u) @ w["wd"][l].float().cpu().T
+        Ks.append(torch.stack(kl))
+        Vs.append(torch.stack(vl))
+    return torch.stack(Ks).numpy(), torch.stack(Vs).numpy()

@@ -12,7 +12,6 @@ import numpy as np
 import pytest
 import torch
 
-from flashact_amd import ma2, pi05
 from flashact_amd.build import DRIVER_PATH
 from tests import ma2_case as M
 from tests import pi05_case as P
@@ -39,26 +38,66 @@ def _run(args):
     return res.stdout
 
 
-def test_cpp_driver_pi05(gpu, tmp_path):
-    NL, Lp, Tv, S, rows = 2, 300, 50, 2, 56
-    c = P.make_case(NL=NL, Lp=Lp, Tv=Tv, S=S, seed=31)
+PI05 = dict(NL=2, Lp=300, Tv=50, S=2, rows=56, seed=31)
+MA2 = dict(NL=2, Lk=493, Tv=30, S=2, adim=6, rows=32, seed=32)
+
+
+def _pi05_files(d):
+    c = P.make_case(NL=PI05["NL"], Lp=PI05["Lp"], Tv=PI05["Tv"], S=PI05["S"], seed=PI05["seed"])
     g = P.gpu_tensors(c, "cpu")
-    d = str(tmp_path)
     for k in ("w1", "wo", "w2", "w3"):
         _write(d, k, g["packed"][k])
     kc, vc = g["caches"][0]
-    x_t = torch.zeros(rows, 32)
-    x_t[:Tv] = c["inp"]["noise"][0]
+    x_t = torch.zeros(PI05["rows"], 32)
+    x_t[:PI05["Tv"]] = c["inp"]["noise"][0]
     for k, t in (("mods", g["mods"]), ("mod_final", g["mod_final"]), ("rope_cos", g["cos"]), ("rope_sin", g["sin"]),
                  ("w_ain", g["w_ain"]), ("b_ain", g["b_ain"]), ("w_aout", g["w_aout"]), ("b_aout", g["b_aout"]),
                  ("kcache", kc), ("vtcache", vc), ("x_t", x_t)):
         _write(d, k, t)
-    out = _run(["pi05", d, NL, Lp, Tv, S, g["Lmax"], rows])
-    assert "cus=256" in out and "coop_max_blocks=256" in out
+    return c, g, ["pi05", d, PI05["NL"], PI05["Lp"], PI05["Tv"], PI05["S"], g["Lmax"], PI05["rows"]]
+
+
+def _ma2_files(d):
+    c = M.make_case(NL=MA2["NL"], Lk=MA2["Lk"], Tv=MA2["Tv"], S=MA2["S"], adim=MA2["adim"], seed=MA2["seed"])
+    g = M.gpu_tensors(c, "cpu")
+    for k, t in zip(("w_qkv", "w_so", "w_cq", "w_co", "w_gu", "w_dn"), g["ws"]):
+        _write(d, k, t)
+    for k, t in zip(("b_qkv", "b_so", "b_cq", "b_co", "b_gu", "b_dn"), g["bs"]):
+        _write(d, k, t)
+    x_t = torch.zeros(MA2["rows"], 32)
+    x_t[:MA2["Tv"]] = c["inp"]["noise"][0]
+    for k, t in (("mods", g["mods"]), ("mod_final", g["mod_final"]), ("rope_cos", g["cos"]), ("rope_sin", g["sin"]),
+                 ("w_ain", g["w_ain"]), ("b_ain", g["b_ain"]), ("w_aout", g["w_aout"]), ("b_aout", g["b_aout"]),
+                 ("kctx", g["kc"][0]), ("vtctx", g["vt"][0]), ("x_t", x_t)):
+        _write(d, k, t)
+    return c, g, ["ma2", d, MA2["NL"], MA2["Lk"], g["Lkmax"], MA2["Tv"], MA2["adim"], MA2["S"], MA2["rows"]]
+
+
+@pytest.fixture(scope="module")
+def drivers(tmp_path_factory):
+    """Both driver processes run here, before any launch of this test process: a child process's
+    cooperative launch is refused by the runtime (hipErrorIllegalState) once its parent process has
+    made cooperative launches of its own, so tests/conftest.py also runs this module first. The GPU
+    is not touched by this process until both children have finished."""
+    import torch as _t
+    if _t.cuda.device_count() == 0:
+        pytest.skip("no GPU visible (GPU tests run on the MI355X box)")
+    out = {}
+    for name, make in (("pi05", _pi05_files), ("ma2", _ma2_files)):
+        d = str(tmp_path_factory.mktemp(name))
+        c, g, args = make(d)
+        out[name] = (c, g, d, _run(args))
+    return out
+
+
+def test_cpp_driver_pi05(drivers, gpu):
+    c, g, d, stdout = drivers["pi05"]
+    Tv, rows, NL = PI05["Tv"], PI05["rows"], PI05["NL"]
+    assert "cus=256" in stdout and "coop_max_blocks=256" in stdout
     xo = np.fromfile(os.path.join(d, "x_t.out"), dtype=np.float32).reshape(rows, 32)
     ref = P.run_oracle(c)[0]
     st = P.parity(xo[:Tv], ref)
-    print(f"C++ driver pi05 NL={NL} Lp={Lp} Tv={Tv} S={S}: {st}", flush=True)
+    print(f"C++ driver pi05 {PI05}: {st}", flush=True)
     assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
     assert np.all(xo[Tv:] == 0.0)
     # the same case through the Python binding: identical actions and suffix cache rows
@@ -69,26 +108,13 @@ def test_cpp_driver_pi05(gpu, tmp_path):
     assert np.array_equal(ko, P.u16(kg)) and np.array_equal(vo, P.u16(vg))
 
 
-def test_cpp_driver_ma2(gpu, tmp_path):
-    NL, Lk, Tv, S, adim, rows = 2, 493, 30, 2, 6, 32
-    c = M.make_case(NL=NL, Lk=Lk, Tv=Tv, S=S, adim=adim, seed=32)
-    g = M.gpu_tensors(c, "cpu")
-    d = str(tmp_path)
-    for k, t in zip(("w_qkv", "w_so", "w_cq", "w_co", "w_gu", "w_dn"), g["ws"]):
-        _write(d, k, t)
-    for k, t in zip(("b_qkv", "b_so", "b_cq", "b_co", "b_gu", "b_dn"), g["bs"]):
-        _write(d, k, t)
-    x_t = torch.zeros(rows, 32)
-    x_t[:Tv] = c["inp"]["noise"][0]
-    for k, t in (("mods", g["mods"]), ("mod_final", g["mod_final"]), ("rope_cos", g["cos"]), ("rope_sin", g["sin"]),
-                 ("w_ain", g["w_ain"]), ("b_ain", g["b_ain"]), ("w_aout", g["w_aout"]), ("b_aout", g["b_aout"]),
-                 ("kctx", g["kc"][0]), ("vtctx", g["vt"][0]), ("x_t", x_t)):
-        _write(d, k, t)
-    _run(["ma2", d, NL, Lk, g["Lkmax"], Tv, adim, S, rows])
+def test_cpp_driver_ma2(drivers):
+    c, g, d, _ = drivers["ma2"]
+    Tv, rows, adim = MA2["Tv"], MA2["rows"], MA2["adim"]
     xo = np.fromfile(os.path.join(d, "x_t.out"), dtype=np.float32).reshape(rows, 32)
     ref = M.run_oracle(c)[0]
     st = M.parity(xo[:Tv], ref, adim)
-    print(f"C++ driver ma2 NL={NL} Lk={Lk} Tv={Tv} S={S}: {st}", flush=True)
+    print(f"C++ driver ma2 {MA2}: {st}", flush=True)
     assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
     assert np.all(xo[Tv:] == 0.0)
     assert np.array_equal(xo[:Tv, adim:], c["inp"]["noise"][0, :, adim:].numpy())

@@ -98,15 +98,16 @@ def test_pi05_rejects_bad_shapes(gpu):
     p = g["packed"]
     kc, vc = g["caches"][0]
     x_t = torch.zeros(65, 32, device=gpu)
-    with pytest.raises(RuntimeError, match="Tv"):
+    # the shim validates sizes before the C ABI does (the C ABI's own checks: tests/test_abi.py)
+    with pytest.raises(ValueError, match="Tv"):
         pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], None, None, None, None, g["mods"], g["mod_final"],
                     g["cos"], g["sin"], g["w_ain"], g["b_ain"], g["w_aout"], g["b_aout"], None, None, 0,
                     kc, vc, 100, g["Lmax"], 1, 65, x_t)
-    with pytest.raises(RuntimeError, match="Lmax"):
+    with pytest.raises(ValueError, match="Lmax"):
         pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], None, None, None, None, g["mods"], g["mod_final"],
                     g["cos"], g["sin"], g["w_ain"], g["b_ain"], g["w_aout"], g["b_aout"], None, None, 0,
                     kc, vc, 100, 112, 1, 20, x_t)
-    with pytest.raises(RuntimeError, match="hand-off"):
+    with pytest.raises(ValueError, match="srows"):
         pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], None, None, None, None, g["mods"], g["mod_final"],
                     g["cos"], g["sin"], g["w_ain"], g["b_ain"], g["w_aout"], g["b_aout"], kc, vc, 10,
                     kc, vc, 100, g["Lmax"], 1, 20, x_t)

@@ -85,6 +85,8 @@ class DeviceInfo(ctypes.Structure):
 # (name, restype, argtypes) of every symbol declared in include/flashact_mi355x.h
 SYMBOLS = [
     ("fa_pi05_denoise", ctypes.c_int, [ctypes.POINTER(Pi05Args), ctypes.c_void_p]),
+    ("fa_pi05_denoise_noalloc", ctypes.c_int,
+     [ctypes.POINTER(Pi05Args), ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
     ("fa_pi05_workspace_bytes", ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     ("fa_pi05_cache_shadow_bytes", ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     ("fa_pi05_workspace_init", ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),

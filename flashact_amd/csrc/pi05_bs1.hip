@@ -40,6 +40,8 @@
 #include "../../include/flashact_mi355x.h"
 #include "fa_host.h"
 
+#include <mutex>
+
 namespace fa {
 namespace pi05 {
 
@@ -1259,6 +1261,13 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
   }
 }
 
+// Scratch of fa_pi05_denoise_noalloc: one workspace in device memory reserved at load time, so
+// that entry point never allocates. Host code reads its address per device with
+// hipGetSymbolAddress and never uses this name as an address.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static_assert(WS_BYTES <= kNoAllocScratchBytes, "the batch-1 workspace fits the static scratch");
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 __global__ void ws_zero(u32x4* p, size_t n16) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
     p[i] = u32x4{0, 0, 0, 0};
@@ -1432,4 +1441,52 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
   if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_pi05_denoise: cooperative launch failed: %s",
                                          hipGetErrorString(e));
   return FA_OK;
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch[64];  // device address of fa::pi05::scratch, per device ordinal (set on first use)
+}  // namespace
+
+extern "C" int fa_pi05_denoise_noalloc(const fa_pi05_args* a, fa_stream_t stream, void** scratch_out) {
+  using namespace fa::pi05;
+  if (!a) return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise_noalloc: args is NULL");
+  if (a->workspace || a->workspace_bytes)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise_noalloc: workspace must be NULL / 0 (this entry point "
+                                          "uses the library's static scratch)");
+  const size_t need = fa_pi05_workspace_bytes(a->batch, a->Tv, a->Lmax);
+  if (need == 0 || need > kNoAllocScratchBytes)
+    return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise_noalloc: batch=%d Tv=%d Lmax=%d needs a %zu-byte workspace; "
+                      "the static scratch holds %zu bytes (use fa_pi05_denoise with a caller workspace)",
+                      a->batch, a->Tv, a->Lmax, need, kNoAllocScratchBytes);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return host::fail(FA_ERR_DEVICE, "fa_pi05_denoise_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return host::fail(FA_ERR_DEVICE, "fa_pi05_denoise_noalloc: device ordinal %d out of range", dev);
+  void* ptr = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+      // First call on this device (current): the scratch's device address, then a fill kernel
+      // zeroes it on the caller's stream ahead of the first launch (the workspace's initial state).
+      void* p = nullptr;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(fa::pi05::scratch));
+      if (e != hipSuccess || !p)
+        return host::fail(FA_ERR_DEVICE, "fa_pi05_denoise_noalloc: hipGetSymbolAddress(scratch): %s",
+                          hipGetErrorString(e));
+      hipLaunchKernelGGL(ws_zero, dim3(1024), dim3(256), 0, (hipStream_t)stream, (u32x4*)p,
+                         kNoAllocScratchBytes / 16);
+      e = hipGetLastError();
+      if (e != hipSuccess)
+        return host::fail(FA_ERR_LAUNCH, "fa_pi05_denoise_noalloc: scratch init: %s", hipGetErrorString(e));
+      g_scratch[dev] = p;
+    }
+    ptr = g_scratch[dev];
+  }
+  if (scratch_out) *scratch_out = ptr;
+  fa_pi05_args b = *a;
+  b.workspace = ptr;
+  b.workspace_bytes = kNoAllocScratchBytes;
+  return fa_pi05_denoise(&b, stream);
 }

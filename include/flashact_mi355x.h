@@ -142,6 +142,18 @@ typedef struct fa_pi05_args {
 /* Whole S-step Euler loop as ONE cooperative launch (256 workgroups, one per CU). */
 int fa_pi05_denoise(const fa_pi05_args* args, fa_stream_t stream);
 size_t fa_pi05_workspace_bytes(int batch, int Tv, int Lmax);
+/* fa_pi05_denoise without a caller workspace. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). args->workspace must be NULL and workspace_bytes 0; the launch uses a
+ * 16 MiB scratch the library reserves in device memory at load time (one per device, held until
+ * the process ends), zeroed by a fill kernel on `stream` at the first call on each device.
+ * Requests whose workspace (fa_pi05_workspace_bytes) exceeds 16 MiB are rejected
+ * (FA_ERR_INVALID_ARG); every batch-1 request fits. No hipMalloc, hipFree or other allocating call
+ * is made. All calls on one device share the scratch, which keeps the last call's contents: calls
+ * that overlap on one GPU race (serialise them on one stream, or use fa_pi05_denoise with one
+ * workspace per concurrent call). *scratch_out (optional) receives the scratch's device address,
+ * for fa_pi05_read_status and fa_pi05_workspace_init. */
+int fa_pi05_denoise_noalloc(const fa_pi05_args* args, fa_stream_t stream, void** scratch_out);
 /* Bytes of the bf16 cache shadow an fp16-cache launch needs (see cache_dtype). */
 size_t fa_pi05_cache_shadow_bytes(int batch, int num_layers, int Lmax);
 /* Zeroes a workspace (required once after allocation and after a non-zero kernel status). */

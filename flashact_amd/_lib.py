@@ -19,6 +19,7 @@ FA_DTYPE_FP8_E4M3 = 1
 FA_DTYPE_F16 = 2
 FA_KSTATUS_SPIN_TIMEOUT = 1
 FA_KSTATUS_XCD_MAP = 2
+FA_KSTATUS_RANGE = 4
 
 
 class FlashActError(RuntimeError):

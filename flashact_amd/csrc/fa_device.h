@@ -37,6 +37,7 @@ constexpr int kRsrcWord3 = 0x00020000;
 // Sticky error bits written into the workspace control block.
 constexpr unsigned kErrSpin = 1u;   // a barrier wait hit its cap
 constexpr unsigned kErrXcd = 2u;    // blockIdx -> XCD mapping differs from the assumed round robin
+constexpr unsigned kErrRange = 4u;  // an exchanged fp16 partial sum exceeded the fp16 range
 constexpr unsigned kSpinCap = 1u << 20;
 
 // Workspace rules shared by every kernel of the library, so that one workspace may serve any mix
@@ -82,6 +83,32 @@ template <int CP>
 __device__ __forceinline__ void stb128(rsrc_t r, uint32_t off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, CP);
 }
+template <int CP>
+__device__ __forceinline__ void stb64(rsrc_t r, uint32_t off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, CP);
+}
+
+// ---------------------------------------------------------------- parity-tagged fp16 exchange
+// Cross-XCD partial sums travel as fp16 whose lowest mantissa bit carries the exchange parity, so
+// data and flag are the same bits (see the batch-1 kernels). Rounding to nearest even and then
+// forcing that bit leaves each value within 2^-10 of its fp32 sum (relative).
+__device__ __forceinline__ unsigned pack_f16x2(float a, float b) {
+  return (unsigned)__builtin_bit_cast(unsigned short, (_Float16)a) |
+         ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)b) << 16);
+}
+// Four fp32 values -> four parity-tagged fp16 (8 bytes). `range` collects |v| > 65504.
+__device__ __forceinline__ u32x2 tag16(f32x4 v, unsigned par, bool& range) {
+  const unsigned pp = par * 0x00010001u;
+  range = range || fabsf(v[0]) > 65504.f || fabsf(v[1]) > 65504.f || fabsf(v[2]) > 65504.f || fabsf(v[3]) > 65504.f;
+  return u32x2{(pack_f16x2(v[0], v[1]) & ~0x00010001u) | pp, (pack_f16x2(v[2], v[3]) & ~0x00010001u) | pp};
+}
+// Non-zero if any of the eight fp16 of v carries the other parity.
+__device__ __forceinline__ unsigned mism16(u32x4 v, unsigned par) {
+  const unsigned pp = par * 0x00010001u;
+  return ((v[0] ^ pp) | (v[1] ^ pp) | (v[2] ^ pp) | (v[3] ^ pp)) & 0x00010001u;
+}
+__device__ __forceinline__ float h_lo(unsigned u) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(u & 0xffffu)); }
+__device__ __forceinline__ float h_hi(unsigned u) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(u >> 16)); }
 
 __device__ __forceinline__ u32x4 ld_stream128(const void* p) {  // weights: read once per step
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));

@@ -14,7 +14,8 @@
 //   [X] = XCD barrier: every compute wave of the XCD stores its epoch to its own flag slot and
 //         polls the XCD's 128 slots (one 16-byte load per lane).
 //   {exchange} = the O / down partial sums are the only data crossing XCDs. Producers store
-//         them with the exchange parity in the lowest mantissa bit of every fp32 value; the
+//         them as fp16 (half the bytes of fp32: the exchange is partly bandwidth-bound) with the
+//         exchange parity in the lowest mantissa bit of every value; the
 //         consumers (N1 / N2 / final norm) poll one 16-byte hint per source XCD (its last-written
 //         values), then read everything and re-read any value whose parity is still stale, so no
 //         grid-wide barrier exists anywhere.
@@ -75,13 +76,13 @@ constexpr uint32_t OFF_ATTP = OFF_Q + NX * TP * HD * 2;             // [8][32 ch
 constexpr uint32_t OFF_ATTML = OFF_ATTP + NX * NCH * TP * HD * 2;   // [8][32][64][2] f32
 constexpr uint32_t OFF_ATTN = OFF_ATTML + NX * NCH * TP * 2 * 4;    // [8][4][8][16][4][8] bf16
 constexpr uint32_t OFF_H = OFF_ATTN + NX * TP * HD * 2;             // [8][4][16][16][4][8] bf16
-constexpr uint32_t OFF_XP = OFF_H + NX * TP * 512 * 2;              // [2][8][64][1024] f32
+constexpr uint32_t OFF_XP = OFF_H + NX * TP * 512 * 2;              // [2][8][64][1024] fp16, parity-tagged
 // This step's own keys/values (the suffix) in MFMA fragment order, per 32-key block of the key
 // range: [8 XCD][3 blocks][2 key tiles][8 k-steps][64 lanes][8 bf16] and
 // [8 XCD][3 blocks][16 dim tiles][2 halves][64 lanes][4 bf16], so attention reads them with
 // contiguous 1 KB / 512 B loads.
 constexpr int NSB = 3;                                              // suffix blocks (Tv <= 64)
-constexpr uint32_t OFF_KFR = OFF_XP + 2 * NX * TP * D * 4;
+constexpr uint32_t OFF_KFR = OFF_XP + 2 * NX * TP * D * 2;
 constexpr uint32_t OFF_VFR = OFF_KFR + NX * NSB * 16384;
 constexpr uint32_t WS_BYTES = OFF_VFR + NX * NSB * 16384;
 static_assert(OFF_XFLAG + NX * NR * NCW * 8 <= kWsCounters, "flags stay below the fixup counters");
@@ -455,28 +456,23 @@ __device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0
 }
 
 // ---------------------------------------------------------------- exchange (cross-XCD)
-__device__ __forceinline__ u32x4 tag(f32x4 v, unsigned par) {
-  u32x4 u = as_u32x4(v);
-#pragma unroll
-  for (int i = 0; i < 4; i++) u[i] = (u[i] & ~1u) | par;
-  return u;
-}
-__device__ __forceinline__ unsigned mism(u32x4 v, unsigned par) {
-  return ((v[0] ^ par) | (v[1] ^ par) | (v[2] ^ par) | (v[3] ^ par)) & 1u;
-}
+// Column d(k) + i (i < 4) of a norm-stage lane, k < 4: the lane's two 16-byte fp16 loads per source
+// XCD cover columns 8 lane + 512 kk + 0..7 (kk < 2), four of them per k.
+__device__ __forceinline__ int ncol(int lane, int k) { return 8 * lane + 512 * (k >> 1) + 4 * (k & 1); }
 
-// Reads the 8 XCD partials of token t, columns 4*lane + 256k (k < 4), from exchange buffer buf.
+// Reads the 8 XCD partials of token t, columns 8*lane + 512kk + 0..7 (kk < 2), from exchange
+// buffer buf (fp16, parity in the lowest mantissa bit).
 // First polls one hint word per source XCD (the 16 bytes written last-in-order by rank 31) with
 // a short sleep between polls, so waiting consumers put almost no load on the fabric; then loads
 // everything once and re-reads (again with a sleep) only the 16-byte groups whose parity is
 // still stale. Correctness rests on the per-value parity check, not on the hint.
-__device__ __forceinline__ void xread(const Ctx& c, int buf, int t, unsigned par, u32x4 (&v)[NX][4], int ts) {
-  const uint32_t b0 = OFF_XP + ((buf * NX * TP + t) * D + 4 * c.lane) * 4;
+__device__ __forceinline__ void xread(const Ctx& c, int buf, int t, unsigned par, u32x4 (&v)[NX][2], int ts) {
+  const uint32_t b0 = OFF_XP + ((buf * NX * TP + t) * D + 8 * c.lane) * 2;
   {
-    const uint32_t hint = c.lane < NX ? OFF_XP + (((buf * NX + c.lane) * TP + t) * D + D - 4) * 4 : OOB;
+    const uint32_t hint = c.lane < NX ? OFF_XP + (((buf * NX + c.lane) * TP + t) * D + D - 8) * 2 : OOB;
     for (unsigned it = 0;; ++it) {
       const u32x4 h = ldb128<kCpSc1>(c.ws, hint);
-      if (__builtin_amdgcn_ballot_w64(c.lane < NX && mism(h, par)) == 0) break;
+      if (__builtin_amdgcn_ballot_w64(c.lane < NX && mism16(h, par)) == 0) break;
       if ((it & 1023) == 1023 &&
           ((__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin) || it > kSpinCap))
         break;
@@ -486,14 +482,14 @@ __device__ __forceinline__ void xread(const Ctx& c, int buf, int t, unsigned par
 #pragma unroll
   for (int gg = 0; gg < NX; gg++)
 #pragma unroll
-    for (int k = 0; k < 4; k++) v[gg][k] = ldb128<kCpSc1>(c.ws, b0 + (gg * TP * D + 256 * k) * 4);
+    for (int k = 0; k < 2; k++) v[gg][k] = ldb128<kCpSc1>(c.ws, b0 + (gg * TP * D + 512 * k) * 2);
   for (unsigned it = 0;; ++it) {
     if (c.tr && c.lane == 0) c.tr[ts == 26 ? 31 : 27] = it;  // traced layer: re-read rounds so far
     unsigned bad = 0;
 #pragma unroll
     for (int gg = 0; gg < NX; gg++)
 #pragma unroll
-      for (int k = 0; k < 4; k++) bad |= mism(v[gg][k], par) << (gg * 4 + k);
+      for (int k = 0; k < 2; k++) bad |= (mism16(v[gg][k], par) != 0u ? 1u : 0u) << (gg * 2 + k);
     if (__builtin_amdgcn_ballot_w64(bad != 0) == 0) break;
     if ((it & 255) == 255) {
       if ((__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin) || it > kSpinCap) {
@@ -505,8 +501,8 @@ __device__ __forceinline__ void xread(const Ctx& c, int buf, int t, unsigned par
 #pragma unroll
     for (int gg = 0; gg < NX; gg++)
 #pragma unroll
-      for (int k = 0; k < 4; k++)
-        if ((bad >> (gg * 4 + k)) & 1u) v[gg][k] = ldb128<kCpSc1>(c.ws, b0 + (gg * TP * D + 256 * k) * 4);
+      for (int k = 0; k < 2; k++)
+        if ((bad >> (gg * 2 + k)) & 1u) v[gg][k] = ldb128<kCpSc1>(c.ws, b0 + (gg * TP * D + 512 * k) * 2);
   }
   asm volatile("" ::: "memory");
   stamp(c, ts);
@@ -515,7 +511,7 @@ __device__ __forceinline__ void xread(const Ctx& c, int buf, int t, unsigned par
 // ---------------------------------------------------------------- norm stages (waves 0, 1)
 // MODE 0: x = embed(x_t) (layer 0).  MODE 1: x += gate * sum_g part_g.  MODE 2: as 1, then the
 // final norm, action projection and Euler update of x_t. Token t = r + 32*wave; lane holds
-// columns 4*lane + 256k + i (k, i < 4).
+// columns ncol(lane, k) + i (k, i < 4).
 template <int MODE>
 __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int buf, unsigned par, const float* gate,
                                            const float* scale, const float* shift, float dt) {
@@ -525,7 +521,7 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int bu
   f32x4 sc[4], sh[4], gt[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const int d = 4 * c.lane + 256 * k;
+    const int d = ncol(c.lane, k);
     sc[k] = *reinterpret_cast<const f32x4*>(scale + d);
     sh[k] = *reinterpret_cast<const f32x4*>(shift + d);
     if (MODE != 0) gt[k] = *reinterpret_cast<const f32x4*>(gate + d);
@@ -553,18 +549,21 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int bu
     }
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      const int d = 4 * c.lane + 256 * k;
+      const int d = ncol(c.lane, k);
       x[k] = *reinterpret_cast<const f32x4*>(xres + d) + *reinterpret_cast<const f32x4*>(p.b_ain + d);
     }
   } else {
-    u32x4 v[NX][4];
+    u32x4 v[NX][2];
     xread(c, buf, t, par, v, buf == 0 ? 26 : 25);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      f32x4 s = as_f32x4(v[0][k]);
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int gg = 1; gg < NX; gg++) s += as_f32x4(v[gg][k]);
-      const f32x4 xo = *reinterpret_cast<const f32x4*>(xres + 4 * c.lane + 256 * k);
+      for (int gg = 0; gg < NX; gg++) {
+        const unsigned lo = v[gg][k >> 1][2 * (k & 1)], hi = v[gg][k >> 1][2 * (k & 1) + 1];
+        s += f32x4{h_lo(lo), h_hi(lo), h_lo(hi), h_hi(hi)};
+      }
+      const f32x4 xo = *reinterpret_cast<const f32x4*>(xres + ncol(c.lane, k));
       x[k] = xo + gt[k] * s;
     }
   }
@@ -581,7 +580,7 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int bu
   if (MODE != 2) {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      const int d = 4 * c.lane + 256 * k;
+      const int d = ncol(c.lane, k);
       *reinterpret_cast<f32x4*>(xres + d) = x[k];
       const u32x2 pk = {pack_bf16x2(h[k][0], h[k][1]), pack_bf16x2(h[k][2], h[k][3])};
       *reinterpret_cast<u32x2*>(p.ws + OFF_XN + c.g * (TP * D * 2) + frag_off(32, t, d)) = pk;
@@ -595,7 +594,7 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int bu
       for (int a = 0; a < 8; a++)
 #pragma unroll
         for (int k = 0; k < 4; k++)
-          wv[a][k] = *reinterpret_cast<const f32x4*>(p.w_aout + (a0 + a) * D + 4 * c.lane + 256 * k);
+          wv[a][k] = *reinterpret_cast<const f32x4*>(p.w_aout + (a0 + a) * D + ncol(c.lane, k));
 #pragma unroll
       for (int a = 0; a < 8; a++) {
         float s = 0.f;
@@ -1039,10 +1038,12 @@ __device__ __forceinline__ void stage_oproj(const Params& p, const Ctx& c, int l
 #pragma unroll
     for (int rt = 0; rt < 2; rt++) acc[rt] *= sc[rt];
   }
+  bool range = false;
 #pragma unroll
   for (int rt = 0; rt < 2; rt++)
-    stb128<kCpSc1>(c.ws, OFF_XP + (((0 * NX + c.g) * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 4,
-                   tag(tv ? acc[rt] : f32x4{0.f, 0.f, 0.f, 0.f}, par));
+    stb64<kCpSc1>(c.ws, OFF_XP + (((0 * NX + c.g) * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 2,
+                  tag16(tv ? acc[rt] : f32x4{0.f, 0.f, 0.f, 0.f}, par, range));
+  if (__builtin_amdgcn_ballot_w64(range) != 0 && c.lane == 0) atomicOr(c.err, kErrRange);
 }
 
 // ---------------------------------------------------------------- gate/up (F-slice g)
@@ -1100,10 +1101,12 @@ __device__ __forceinline__ void stage_dn(const Params& p, const Ctx& c, int l, i
 #pragma unroll
     for (int rt = 0; rt < 2; rt++) acc[rt] *= sc[rt];
   }
+  bool range = false;
 #pragma unroll
   for (int rt = 0; rt < 2; rt++)
-    stb128<kCpSc1>(c.ws, OFF_XP + (((1 * NX + c.g) * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 4,
-                   tag(tv ? acc[rt] : f32x4{0.f, 0.f, 0.f, 0.f}, par));
+    stb64<kCpSc1>(c.ws, OFF_XP + (((1 * NX + c.g) * TP + t) * D + 32 * c.r + rt * 16 + 4 * c.lq) * 2,
+                  tag16(tv ? acc[rt] : f32x4{0.f, 0.f, 0.f, 0.f}, par, range));
+  if (__builtin_amdgcn_ballot_w64(range) != 0 && c.lane == 0) atomicOr(c.err, kErrRange);
 }
 
 // ---------------------------------------------------------------- instrumentation
@@ -1155,7 +1158,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
     // buffers with any parity. The compute waves clear them (parity 0), restart the parity
     // sequence and pass one grid barrier before the first exchange.
     xbase = 0;
-    constexpr uint32_t n16 = 2u * NX * TP * D * 4 / 16;
+    constexpr uint32_t n16 = 2u * NX * TP * D * 2 / 16;
     for (uint32_t i = blockIdx.x * (NCW * 64) + tid; i < n16; i += NWG * NCW * 64)
       stb128<kCpSc1>(c.ws, OFF_XP + 16 * i, u32x4{0u, 0u, 0u, 0u});
     __builtin_amdgcn_s_waitcnt(0);

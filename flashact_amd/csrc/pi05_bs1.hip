@@ -77,14 +77,14 @@ constexpr uint32_t OFF_ATTML = OFF_ATTP + NX * NCH * TP * HD * 2;   // [8][32][6
 constexpr uint32_t OFF_ATTN = OFF_ATTML + NX * NCH * TP * 2 * 4;    // [8][4][8][16][4][8] bf16
 constexpr uint32_t OFF_H = OFF_ATTN + NX * TP * HD * 2;             // [8][4][16][16][4][8] bf16
 constexpr uint32_t OFF_XP = OFF_H + NX * TP * 512 * 2;              // [2][8][64][1024] fp16, parity-tagged
-// This step's own keys/values (the suffix) in MFMA fragment order, per 32-key block of the key
-// range: [8 XCD][3 blocks][2 key tiles][8 k-steps][64 lanes][8 bf16] and
-// [8 XCD][3 blocks][16 dim tiles][2 halves][64 lanes][4 bf16], so attention reads them with
-// contiguous 1 KB / 512 B loads.
-constexpr int NSB = 3;                                              // suffix blocks (Tv <= 64)
-constexpr uint32_t OFF_KFR = OFF_XP + 2 * NX * TP * D * 2;
-constexpr uint32_t OFF_VFR = OFF_KFR + NX * NSB * 16384;
-constexpr uint32_t WS_BYTES = OFF_VFR + NX * NSB * 16384;
+// This step's own keys/values (the suffix), token t held by attention rank t % 32 as its slot t / 32:
+// K [8 XCD][32 ranks][2 slots][256 dims] (one slot = one 512-byte key row, so a lane of the
+// attention MFMA's A fragment loads 16 contiguous bytes) and V [8 XCD][32 ranks][16][16][2]
+// (dim 16 dt + lr of both slots at ((rank 16 + lr) 16 + dt) 4 bytes: a lane's 16 dims are 64
+// contiguous bytes).
+constexpr uint32_t OFF_KS = OFF_XP + 2 * NX * TP * D * 2;
+constexpr uint32_t OFF_VS = OFF_KS + NX * NR * 2 * HD * 2;
+constexpr uint32_t WS_BYTES = OFF_VS + NX * NR * 2 * HD * 2;
 static_assert(OFF_XFLAG + NX * NR * NCW * 8 <= kWsCounters, "flags stay below the fixup counters");
 
 // LDS layout (bytes)
@@ -651,13 +651,10 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
     if (vr0 >= 512) {
       if (!tv) continue;
       const int d = vr0 - 512;
-      // value dims d..d+3 of key Lp+t into the XCD's copy of its 32-key block, laid out as the V^T
-      // ring page: dim tile d/16, lane d%16 + 16 (j/8), element j%8 for key offset j
-      const int kp = p.Lp + t, st = (kp >> 5) - (p.Lp >> 5), j = kp & 31;
-      bf16* vf = reinterpret_cast<bf16*>(p.ws + OFF_VFR + (c.g * NSB + st) * 16384) +
-                 ((d >> 4) * 64 + (d & 15) + 16 * (j >> 3)) * 8 + (j & 7);
+      // value dims d..d+3 of this step's token t into the XCD's copy: rank t % 32, slot t / 32
+      bf16* vf = reinterpret_cast<bf16*>(p.ws + OFF_VS) + ((c.g * NR + (t & 31)) * 16) * 32 + (t >> 5);
 #pragma unroll
-      for (int i = 0; i < 4; i++) vf[i * 8] = (bf16)v[i];
+      for (int i = 0; i < 4; i++) vf[(((d + i) & 15) * 16 + ((d + i) >> 4)) * 2] = (bf16)v[i];
       if (last && c.g == (l & 7)) {
         bf16* vr = p.vtcache + ((size_t)l * HD + d) * p.Lmax + p.Lp + t;
 #pragma unroll
@@ -677,14 +674,12 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
       *reinterpret_cast<unsigned*>(p.ws + qb + frag_off(8, t, j)) = plo;
       *reinterpret_cast<unsigned*>(p.ws + qb + frag_off(8, t, j + 128)) = phi;
     } else {
-      // Every XCD keeps its own fragment-ordered copy of this step's keys for attention. The
-      // caller's cache rows (the reference leaves the last step's suffix K/V there) are written
+      // Every XCD keeps its own copy of this step's keys for attention (rank t % 32, slot t / 32).
+      // The caller's cache rows (the reference leaves the last step's suffix K/V there) are written
       // in the last step only, by XCD l % 8.
-      const int kp = p.Lp + t, st = (kp >> 5) - (p.Lp >> 5), jk = kp & 31;
-      const uint32_t kb = OFF_KFR + (((c.g * NSB + st) * 2 + (jk >> 4)) * 8) * 1024 + (jk & 15) * 16;
-      // dims j, j+1 (lo) and j+128, j+129 (hi): k-step d/32, lane quarter (d%32)/8, element d%8
-      *reinterpret_cast<unsigned*>(p.ws + kb + (j >> 5) * 1024 + ((j & 31) >> 3) * 256 + (j & 7) * 2) = plo;
-      *reinterpret_cast<unsigned*>(p.ws + kb + ((j + 128) >> 5) * 1024 + ((j & 31) >> 3) * 256 + (j & 7) * 2) = phi;
+      bf16* kf = reinterpret_cast<bf16*>(p.ws + OFF_KS) + ((c.g * NR + (t & 31)) * 2 + (t >> 5)) * HD;
+      *reinterpret_cast<unsigned*>(kf + j) = plo;
+      *reinterpret_cast<unsigned*>(kf + j + 128) = phi;
       if (last && c.g == (l & 7)) {
         bf16* kr = p.kcache + ((size_t)l * p.Lmax + p.Lp + t) * HD;
         *reinterpret_cast<unsigned*>(kr + j) = plo;
@@ -695,75 +690,26 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
 }
 
 // ---------------------------------------------------------------- attention partials
-// This step's keys inside a rank's first 32-key block go from the XCD's suffix copies (written by
-// QKV) into the K and V^T ring pages, over the rows the loader brought from the caches, so the
-// whole block is then read from LDS. The four compute waves share the copy (4 fragments of each
-// page per wave, one L2 round trip) and meet on an LDS counter that reaches `target`. A V^T lane
-// slot holds 8 keys; one that straddles Lp keeps its prefix elements from the page.
-__device__ __forceinline__ void stage_suffix(const Params& p, const Ctx& c, int kb, int pgk, unsigned target) {
-  const int st = (kb >> 5) - (p.Lp >> 5);
-  const uint32_t kslot = (pgk % RING) * PAGE, vslot = ((pgk + 1) % RING) * PAGE;
-  const uint32_t kfr = OFF_KFR + (c.g * NSB + st) * 16384, vfr = OFF_VFR + (c.g * NSB + st) * 16384;
-  const bool ksfx = kb + 16 * (c.wave >> 1) + c.lr >= p.Lp;  // key row of this lane in fragments 4w..4w+3
-  const int npre = min(max(p.Lp - (kb + 8 * c.lq), 0), 8);    // prefix keys of this lane's V^T slot
-  u32x4 kv[4], vv[4], pv[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const uint32_t f = 4 * c.wave + i;
-    kv[i] = ldb128<kCpSc1>(c.ws, ksfx ? kfr + f * 1024 + c.lane * 16 : OOB);
-    vv[i] = ldb128<kCpSc1>(c.ws, npre < 8 ? vfr + f * 1024 + c.lane * 16 : OOB);
-    pv[i] = *reinterpret_cast<const u32x4*>(fa_lds + vslot + f * 1024 + c.lane * 16);
-  }
-  unsigned keep[4];  // page elements kept: element e of the slot is key kb + 8 lq + e
-#pragma unroll
-  for (int m = 0; m < 4; m++) keep[m] = (2 * m < npre ? 0xffffu : 0u) | (2 * m + 1 < npre ? 0xffff0000u : 0u);
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const uint32_t f = 4 * c.wave + i;
-    if (ksfx) *reinterpret_cast<u32x4*>(fa_lds + kslot + f * 1024 + c.lane * 16) = kv[i];
-    if (npre < 8) {
-      u32x4 o;
-#pragma unroll
-      for (int m = 0; m < 4; m++) o[m] = (pv[i][m] & keep[m]) | (vv[i][m] & ~keep[m]);
-      *reinterpret_cast<u32x4*>(fa_lds + vslot + f * 1024 + c.lane * 16) = o;
-    }
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's page writes are done
-  unsigned* cnt = reinterpret_cast<unsigned*>(fa_lds + L_CTL) + 8;
-  if (c.lane == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  for (unsigned it = 0;; ++it) {
-    if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target || ctl_ld(6)) break;
-    if (it > kSpinCap) {
-      ctl_st(6, 1u);
-      if (c.lane == 0) atomicOr(c.err, kErrSpin);
-      break;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
-  asm volatile("" ::: "memory");  // page reads stay after the meeting
-}
-
-// Head g, keys [kbeg, kend) of chunk r (C = 32 ceil(Ltot/1024) keys), tokens of this wave's tile,
-// in 32-key blocks. Sources per key (K rows) or 4-key group (V^T columns): prefix keys of the
-// first block come from the LDS pages the loader prefetched, prefix keys of later blocks from the
-// caches, this step's keys from the XCD-private fragment-ordered copies; a 4-key group that
-// straddles Lp takes its prefix and suffix elements from both. Keys past kend: S = -inf, V = 0.
-__device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, int pgk, int li) {
-  const int Ltot = p.Lp + p.Tv;
-  const int C = 32 * ((Ltot + 32 * NCH - 1) / (32 * NCH));
-  const int kbeg = c.kb0, kend = min(kbeg + C, Ltot);
+// Head g, chunk r: the prefix keys [kbeg, kend) of the chunk (C = 32 ceil(Lp / 1024) keys per rank)
+// in 32-key blocks -- the first from the LDS pages the loader prefetched, later ones from the
+// caches -- then this step's keys of tokens r and r + 32 (those below Tv) from the XCD's suffix
+// copies, as one more block. Spreading this step's keys over all ranks keeps every rank's stage the
+// same length (measured: the two ranks that held all of them ran 4.6 us against 2.8 us); their
+// loads are issued after the last prefix block's S^T MFMAs (issued with q instead, they keep 48
+// more VGPRs live through the prefix blocks, and the stage measured slower). Keys past kend:
+// S = -inf, V = 0.
+__device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, int pgk) {
+  const int C = 32 * max(1, (p.Lp + 32 * NCH - 1) / (32 * NCH));
+  const int kbeg = c.kb0, kend = min(kbeg + C, p.Lp);
+  const int nsfx = (c.r < p.Tv ? 1 : 0) + (c.r + 32 < p.Tv ? 1 : 0);  // this step's keys of this rank
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
-  if (kbeg < kend && min(kbeg + 32, kend) > p.Lp) {  // the first block holds keys of this step
-    page_wait(c, pgk + 1);
-    stage_suffix(p, c, kbeg, pgk, 4u * (unsigned)(li + 1));
-  }
   if (16 * c.wave >= p.Tv) {
     page_release(c, pgk + 2);
     return;
   }
   const uint32_t pbase = ((c.g * NCH + c.r) * TP + t);
-  if (kbeg >= kend) {  // empty chunk: weight 0 in the combine
+  if (kbeg >= kend && nsfx == 0) {  // empty chunk: weight 0 in the combine
     if (tv && c.lq == 0) {
       const f32x2 ml = {-1e30f, 0.f};
       *reinterpret_cast<f32x2*>(p.ws + OFF_ATTML + pbase * 8) = ml;
@@ -778,6 +724,18 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) qf[ks] = ldb128<kCpSc1>(c.ws, qb + ks * 1024);
   }
+  // this step's keys of this rank: K rows (slot = MFMA row lr < nsfx, other rows zero) and the two
+  // slots of V for dims 16 dt + lr (lanes of quarter 0), requested by issue_suffix()
+  u32x4 skf[8], svf[4];
+  const uint32_t ks0 = OFF_KS + (c.g * NR + c.r) * (2 * HD * 2);
+  const uint32_t vs0 = OFF_VS + ((c.g * NR + c.r) * 16 + c.lr) * 64;
+  auto issue_suffix = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+      skf[ks] = ldb128<kCpSc1>(c.ws, c.lr < nsfx ? ks0 + c.lr * (HD * 2) + (32 * ks + 8 * c.lq) * 2 : OOB);
+#pragma unroll
+    for (int j = 0; j < 4; j++) svf[j] = ldb128<kCpSc1>(c.ws, c.lq == 0 && nsfx > 0 ? vs0 + 16 * j : OOB);
+  };
   page_wait(c, pgk + 1);
   stamp(c, 23);
   const uint32_t kslot = (pgk % RING) * PAGE, vslot = ((pgk + 1) % RING) * PAGE;
@@ -789,26 +747,22 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
   const uint32_t kl = (uint32_t)l * p.Lmax * HD * 2;  // layer base, kcache [Lmax][256]
   const uint32_t vl = (uint32_t)l * HD * p.Lmax * 2;  // layer base, vtcache [256][Lmax]
   const uint32_t vstep = 16 * p.Lmax * 2;             // 16 dims
+  if (kbeg >= kend) issue_suffix();
 #pragma unroll 1
   for (int kb = kbeg; kb < kend; kb += 32) {
     const bool first = kb == kbeg;
-    const int st = (kb >> 5) - (p.Lp >> 5);  // suffix block of this 32-key block (if it has suffix keys)
     const int kg0 = kb + c.lq * 4;
     f32x4 s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
       u32x4 kf[8];
       const int key = kb + kt * 16 + c.lr;
-      if (first) {  // the ring page (this step's keys staged into it)
+      if (first) {  // the ring page
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
           kf[ks] = *reinterpret_cast<const u32x4*>(fa_lds + kslot + (kt * 8 + ks) * 1024 + c.lane * 16);
-      } else if (key >= p.Lp) {
-        const uint32_t rb = key < kend ? OFF_KFR + (((c.g * NSB + st) * 2 + kt) * 8) * 1024 + c.lane * 16 : OOB;
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) kf[ks] = ldb128<kCpSc1>(c.ws, rb + ks * 1024);
       } else {
-        const uint32_t rb = kl + key * HD * 2 + c.lq * 16;
+        const uint32_t rb = key < kend ? kl + key * HD * 2 + c.lq * 16 : OOB;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) kf[ks] = ldb128<kCpPlain>(c.kc, rb + ks * 64);
       }
@@ -818,6 +772,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
       for (int ks = 0; ks < 8; ks++) a = mfma16(kf[ks], qf[ks], a);
       s[kt] = a;
     }
+    if (kb + 32 >= kend) issue_suffix();  // last prefix block: this step's keys arrive under its P V
     if (c.tr) stamp(c, first ? 29 : 30);
     // lane holds S^T[key kb + 16kt + 4lq + i][token lr]
     float bmax = -1e30f;
@@ -851,13 +806,11 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
     // B operand P^T: k-slot 8lq+i <-> key kg0+i (i<4), kg0+16+(i-4) (i>=4); V^T uses the same order
     const u32x4 pb = {pk[0], pk[1], pk[2], pk[3]};
     unsigned vm[2][2];  // zero V elements of keys >= kend inside a partially valid 4-key group
-    int npre[2];        // keys of each 4-key group inside the prefix
 #pragma unroll
     for (int h2 = 0; h2 < 2; h2++) {
       const int nv = min(max(kend - (kg0 + 16 * h2), 0), 4);
       vm[h2][0] = nv >= 2 ? 0xffffffffu : (nv == 1 ? 0xffffu : 0u);
       vm[h2][1] = nv >= 4 ? 0xffffffffu : (nv == 3 ? 0xffffu : 0u);
-      npre[h2] = min(max(p.Lp - (kg0 + 16 * h2), 0), 4);
     }
     // V^T operand (dim 16dt+lr, keys kg0 + 16h + (0..3)) in two halves of 8 dim tiles
 #pragma unroll
@@ -867,35 +820,15 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
 #pragma unroll
       for (int h2 = 0; h2 < 2; h2++) {
         const int kg = kg0 + 16 * h2;
-        if (first) {  // the ring page (this step's keys staged into it)
+        if (first) {  // the ring page
           const int o8 = 16 * h2 + 4 * c.lq;  // key offset within the 32-key block
           const uint32_t ad = vslot + (c.lr + 16 * (o8 >> 3)) * 16 + (o8 & 7) * 2 + half * 8 * 1024;
 #pragma unroll
           for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = *reinterpret_cast<const u32x2*>(fa_lds + ad + d8 * 1024);
-          continue;
-        }
-        if (npre[h2] > 0) {  // prefix elements from the cache
-          const uint32_t vo = vl + c.lr * p.Lmax * 2 + kg * 2 + half * 8 * vstep;
+        } else {
+          const uint32_t vo = kg < kend ? vl + c.lr * p.Lmax * 2 + kg * 2 + half * 8 * vstep : OOB;
 #pragma unroll
           for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = ldb64<kCpPlain>(c.vc, vo + d8 * vstep);
-        }
-        if (npre[h2] < 4) {  // this step's elements from the XCD's copy (V^T page layout)
-          const uint32_t vo = kg < kend ? OFF_VFR + (c.g * NSB + st) * 16384 +
-                                              (half * 8 * 64 + c.lr + 16 * (2 * h2 + (c.lq >> 1))) * 16 + 8 * (c.lq & 1)
-                                        : OOB;
-          if (npre[h2] == 0) {
-#pragma unroll
-            for (int d8 = 0; d8 < 8; d8++) vf[d8][h2] = ldb64<kCpSc1>(c.ws, vo + d8 * 1024);
-          } else {  // the group straddles Lp: merge element-wise
-            const unsigned pm0 = npre[h2] >= 2 ? 0xffffffffu : 0xffffu;
-            const unsigned pm1 = npre[h2] == 3 ? 0xffffu : 0u;
-#pragma unroll
-            for (int d8 = 0; d8 < 8; d8++) {
-              const u32x2 b = ldb64<kCpSc1>(c.ws, vo + d8 * 1024);
-              vf[d8][h2][0] = (vf[d8][h2][0] & pm0) | (b[0] & ~pm0);
-              vf[d8][h2][1] = (vf[d8][h2][1] & pm1) | (b[1] & ~pm1);
-            }
-          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);  // the half's V^T fragments are all requested before its MFMAs
@@ -906,6 +839,39 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
                           vf[d8][1][1] & vm[1][1]};
         o[dt] = mfma16(va, pb, o[dt] * alpha);
       }
+    }
+  }
+  if (nsfx > 0) {
+    // This step's keys: one 16-key S^T tile whose rows 0 (token r) and 1 (token r + 32) are valid;
+    // P^T k-slots 8lq + i hold keys 4lq + i (i < 4), so only slots 0, 1 of quarter 0 are non-zero,
+    // and the V^T operand of lane (lr, quarter 0) is dim 16 dt + lr of both slots.
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) a = mfma16(skf[ks], qf[ks], a);
+    float sv[4], bmax = -1e30f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      sv[i] = (c.lq == 0 && i < nsfx) ? a[i] * qscale : -1e30f;
+      bmax = fmaxf(bmax, sv[i]);
+    }
+    bmax = cols_max(bmax);
+    const float mnew = fmaxf(m, bmax);
+    const float alpha = exp2_w(m - mnew);
+    m = mnew;
+    float pv[4], psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      pv[i] = exp2_w(sv[i] - m);
+      psum += pv[i];
+    }
+    psum = cols_sum(psum);
+    lsum = lsum * alpha + psum;
+    const u32x4 pb = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), 0u, 0u};
+    const unsigned slot_mask = nsfx == 2 ? 0xffffffffu : 0xffffu;  // slot 1 is stale without token r + 32
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++) {
+      const u32x4 va = {svf[dt >> 2][dt & 3] & slot_mask, 0u, 0u, 0u};
+      o[dt] = mfma16(va, pb, o[dt] * alpha);
     }
   }
   stamp(c, 24);
@@ -1130,7 +1096,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
   c.lq = c.lane >> 4;
   c.g = blockIdx.x & 7;
   c.r = blockIdx.x >> 3;
-  c.kb0 = c.r * 32 * ((p.Lp + p.Tv + 32 * NCH - 1) / (32 * NCH));
+  c.kb0 = c.r * 32 * max(1, (p.Lp + 32 * NCH - 1) / (32 * NCH));
   c.ws = make_rsrc(p.ws, WS_BYTES);
   c.kc = make_rsrc(p.kcache, (uint32_t)((size_t)p.NL * p.Lmax * HD * 2));
   c.vc = make_rsrc(p.vtcache, (uint32_t)((size_t)p.NL * p.Lmax * HD * 2));
@@ -1207,7 +1173,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       launder(c);
       mark(p, c, 9, t0);
       stamp(c, 4);
-      stage_att(p, c, l, pb + PG::K, li);
+      stage_att(p, c, l, pb + PG::K);
       stamp(c, 5);
       mark(p, c, 2, t0);
       xcd_sync(p, c);

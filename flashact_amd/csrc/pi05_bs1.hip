@@ -11,8 +11,10 @@
 //   XCD g owns query head g, the MLP columns f in [512g, 512g+512) and the K-windows g of the
 //   O and down projections. Per layer (sync after each stage in brackets):
 //     N1 [X] QKV [X] ATT [X] COMB [X] O {exchange} N2 [X] GU [X] DN {exchange}
-//   [X] = XCD barrier: every compute wave of the XCD stores its epoch to its own flag slot and
-//         polls the XCD's 128 slots (one 16-byte load per lane).
+//   [X] = XCD sync point: every compute wave of the XCD stores its epoch to its own flag slot. Before
+//         ATT and COMB (whose waves read every rank's output) each wave polls the XCD's 128 slots;
+//         before QKV, O, GU and DN each wave polls only the waves that wrote its operand rows
+//         (DN: one group of 16 gate/up ranks per 8-k-step chunk of its K loop).
 //   {exchange} = the O / down partial sums are the only data crossing XCDs. Producers store
 //         them as fp16 (half the bytes of fp32: the exchange is partly bandwidth-bound) with the
 //         exchange parity in the lowest mantissa bit of every value; the
@@ -164,12 +166,20 @@ __device__ __forceinline__ void ctl_st(int i, unsigned v) {
 }
 
 // ---------------------------------------------------------------- XCD barrier (per wave)
-__device__ __forceinline__ void xcd_sync(const Params& p, Ctx& c) {
+// A sync point: the wave drains its stores (they have reached L2) and publishes its epoch to its
+// own flag slot. xcd_sync then waits for every compute wave of the XCD; a stage whose waves need
+// only some producers waits for those instead (xcd_wait_ranks), so it starts as soon as its own
+// inputs are complete rather than when the slowest wave of the XCD is done.
+__device__ __forceinline__ void xcd_signal(const Params& p, Ctx& c) {
   __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have reached L2
   c.e += 1;
   if (c.lane == 0)
     __hip_atomic_store(reinterpret_cast<uint64_t*>(p.ws + OFF_XFLAG) + (c.g * NR + c.r) * NCW + c.wave, c.e,
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void xcd_sync(const Params& p, Ctx& c) {
+  xcd_signal(p, c);
   if (__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin) return;
   const uint32_t off = OFF_XFLAG + c.g * (NR * NCW * 8) + c.lane * 16;
   for (unsigned it = 0;; ++it) {
@@ -185,6 +195,29 @@ __device__ __forceinline__ void xcd_sync(const Params& p, Ctx& c) {
   }
   asm volatile("" ::: "memory");  // loads after the barrier stay after it
 }
+
+// Waits until compute wave `wv` of ranks [r0, r0 + n) of this XCD (n <= 32) has passed the sync
+// point this wave passed last (epoch c.e).
+__device__ __forceinline__ void xcd_wait_ranks(const Ctx& c, int r0, int n, int wv) {
+  if (__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin) return;
+  const bool mine = c.lane < n;
+  const uint32_t off = mine ? OFF_XFLAG + ((c.g * NR + r0 + c.lane) * NCW + wv) * 8 : OOB;
+  for (unsigned it = 0;; ++it) {
+    const u32x2 v = ldb64<kCpSc1>(c.ws, off);
+    const uint64_t a = ((uint64_t)v[1] << 32) | v[0];
+    if (__builtin_amdgcn_ballot_w64(mine && a < c.e) == 0) break;
+    if (it > kSpinCap) {
+      if (c.lane == 0) atomicOr(c.err, kErrSpin);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");  // loads after the wait stay after it
+}
+
+// Waits for the norm waves that wrote the operand rows of this wave's token tile (token t is
+// normed by rank t % 32, wave t / 32).
+__device__ __forceinline__ void wait_norm_rows(const Ctx& c) { xcd_wait_ranks(c, 16 * (c.wave & 1), 16, c.wave >> 1); }
 
 // ---------------------------------------------------------------- weight ring
 // Compute wave side: wait until both loader waves have landed page pg; release pages < upto.
@@ -396,14 +429,20 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16(unsigned lo, unsigned hi) {
 // so k-step ks reads 8 bytes at 16 lr + 256 (2 (ks%2) + lq/2) + 8 (lq%2). xoff = byte offset in the
 // workspace of X[token][k = 8 lq] (OOB for tokens >= Tv: the loads return zeros); k-step ks adds
 // XSTRIDE bytes.
-template <int RT, int KS, int XSTRIDE = 64, bool FP8 = false, int PRT = KS / 2>
-__device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0, uint32_t xoff, int ts) {
+struct NoWait {
+  __device__ void operator()(int) const {}
+};
+
+template <int RT, int KS, int XSTRIDE = 64, bool FP8 = false, int PRT = KS / 2, class Wait = NoWait>
+__device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0, uint32_t xoff, int ts,
+                                         const Wait& wait = Wait()) {
   // Software-pipelined in chunks of 8 k-steps: the loads of chunk i+1 are in flight while the
   // MFMAs of chunk i run, so compute starts as soon as the first operands arrive.
   constexpr int NPG = FP8 ? (RT * PRT + 15) / 16 : (RT * KS + 15) / 16;
   constexpr int KC = KS < 8 ? KS : 8;
   constexpr int NCK = KS / KC;
   u32x4 xf[2][KC];
+  wait(0);  // the producers of chunk 0's operand rows are done
 #pragma unroll
   for (int k = 0; k < KC; k++) xf[0][k] = ldb128<kCpSc1>(c.ws, xoff + k * XSTRIDE);
   // two accumulators per row tile (even / odd k-steps) keep four independent MFMA chains in flight
@@ -419,6 +458,7 @@ __device__ __forceinline__ void gemm_tok(f32x4 (&acc)[RT], const Ctx& c, int pg0
 #pragma unroll
   for (int ck = 0; ck < NCK; ck++) {
     if (ck + 1 < NCK) {
+      wait(ck + 1);
 #pragma unroll
       for (int k = 0; k < KC; k++) xf[(ck + 1) & 1][k] = ldb128<kCpSc1>(c.ws, xoff + ((ck + 1) * KC + k) * XSTRIDE);
     }
@@ -637,7 +677,9 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
   if (any)
     gemm_tok<2, 32, 1024, FP8, 16>(acc, c, pg0, tv ? OFF_XN + c.g * (TP * D * 2) + frag_off(32, t, 8 * c.lq) : OOB,
-                                   15);
+                                   15, [&c](int ck) {
+                                     if (ck == 0) wait_norm_rows(c);
+                                   });
   page_release(c, pg0 + Pages<FP8>::NQKV);
   if constexpr (FP8) {
 #pragma unroll
@@ -998,7 +1040,8 @@ __device__ __forceinline__ void stage_oproj(const Params& p, const Ctx& c, int l
   }
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
   if (16 * c.wave < p.Tv)
-    gemm_tok<2, 8, 1024, FP8, 8>(acc, c, pg, tv ? OFF_ATTN + c.g * (TP * HD * 2) + frag_off(8, t, 8 * c.lq) : OOB, 17);
+    gemm_tok<2, 8, 1024, FP8, 8>(acc, c, pg, tv ? OFF_ATTN + c.g * (TP * HD * 2) + frag_off(8, t, 8 * c.lq) : OOB, 17,
+                                 [&c](int) { xcd_wait_ranks(c, 8 * c.wave, 8, 0); });  // the combine of this tile
   page_release(c, pg + 1);
   if constexpr (FP8) {
 #pragma unroll
@@ -1029,7 +1072,9 @@ __device__ __forceinline__ void stage_gu(const Params& p, const Ctx& c, int l, i
   }
   f32x4 acc[2];
   gemm_tok<2, 32, 1024, FP8, 16>(acc, c, pg0, tv ? OFF_XN + c.g * (TP * D * 2) + frag_off(32, t, 8 * c.lq) : OOB,
-                                 19);
+                                 19, [&c](int ck) {
+                                   if (ck == 0) wait_norm_rows(c);
+                                 });
   page_release(c, pg0 + Pages<FP8>::NGU);
   if (!tv) return;
   if constexpr (FP8) {
@@ -1061,7 +1106,11 @@ __device__ __forceinline__ void stage_dn(const Params& p, const Ctx& c, int l, i
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
   if (16 * c.wave < p.Tv)
     gemm_tok<2, 16, 1024, FP8, 8>(acc, c, pg0, tv ? OFF_H + c.g * (TP * 512 * 2) + frag_off(16, t, 8 * c.lq) : OOB,
-                                  21);
+                                  21, [&c](int ck) {
+                                    // k-steps 8ck..8ck+7 are h columns 256ck.. of this XCD's F slice,
+                                    // written by wave w of gate/up ranks 16ck..16ck+15
+                                    xcd_wait_ranks(c, 16 * ck, 16, c.wave);
+                                  });
   page_release(c, pg0 + Pages<FP8>::NDN);
   if constexpr (FP8) {
 #pragma unroll
@@ -1162,7 +1211,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       }
       stamp(c, 1);
       mark(p, c, 0, t0);
-      xcd_sync(p, c);
+      xcd_signal(p, c);  // QKV waves wait for the norm waves of their tile
       launder(c);
       mark(p, c, 9, t0);
       stamp(c, 2);
@@ -1183,7 +1232,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       stage_comb(p, c, li);
       stamp(c, 7);
       mark(p, c, 3, t0);
-      xcd_sync(p, c);
+      xcd_signal(p, c);  // O waves wait for the combine of their tile
       launder(c);
       mark(p, c, 9, t0);
       stamp(c, 8);
@@ -1193,14 +1242,14 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       if (nw) stage_norm<1>(p, c, 0, par, mod_in + 2 * D, mod_post, mod_post + D, 0.f);
       stamp(c, 10);
       mark(p, c, 5, t0);
-      xcd_sync(p, c);
+      xcd_signal(p, c);  // gate/up waves wait for the norm waves of their tile
       launder(c);
       mark(p, c, 9, t0);
       stamp(c, 11);
       stage_gu<FP8>(p, c, l, pb + PG::GU);
       stamp(c, 12);
       mark(p, c, 6, t0);
-      xcd_sync(p, c);
+      xcd_signal(p, c);  // down waves wait, k-chunk by k-chunk, for the gate/up ranks of it
       launder(c);
       mark(p, c, 9, t0);
       stamp(c, 13);

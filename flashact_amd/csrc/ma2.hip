@@ -130,12 +130,13 @@ struct FinSiluGate {  // columns 2f, 2f+1 = gate f, up f -> h[m][f] = silu(g + b
 };
 
 struct EpiPartN : NoPre {  // fp32 partial sums [split][MP][N] (summed by the consumer stage)
+  static constexpr int kRowBytes = 16;
+  static constexpr bool kStaged = true;
   rsrc_t ws;
   uint32_t off;
   int MP, N, split;
-  __device__ void operator()(int n0, int m, f32x4 v, Pre) const {
-    st_b128(ws, off + (uint32_t)((((size_t)split * MP + m) * N + n0) * 4), as_u32x4(v));
-  }
+  __device__ u32x4 pack(int, f32x4 v) const { return as_u32x4(v); }
+  __device__ uint32_t row_off(int m, int n0) const { return off + (uint32_t)((((size_t)split * MP + m) * N + n0) * 4); }
 };
 
 // acc[q] += sum over the `ks` fp32 partial rows [s][MP][N] of row m, columns c[q]..c[q]+3; PB

@@ -30,6 +30,8 @@ __host__ __device__ inline uint32_t qf_off(int NQT, int b, int r, int d) {
 // adjacent), 256 v. RoPE at table row t; q -> fragment-ordered Q, k -> kcache row Lp + t, v ->
 // vtcache column Lp + t of layer l.
 struct EpiQKV {
+  static constexpr int kRowBytes = 0;
+  static constexpr bool kStaged = false;
   rsrc_t ws, kc, vc;
   const float* rcos;
   const float* rsin;

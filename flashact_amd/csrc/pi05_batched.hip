@@ -85,22 +85,25 @@ struct Params {
 };
 
 struct EpiGelu : NoPre {  // rows 2f, 2f+1 = gate f, up f -> h[m][f] = gelu_tanh(g) u
+  static constexpr int kRowBytes = 4;
+  static constexpr bool kStaged = false;
   rsrc_t ws;
   uint32_t off;
   int split;
-  __device__ void operator()(int n0, int m, f32x4 v, Pre) const {
-    const unsigned pk = pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]);
-    st_b32(ws, off + (uint32_t)(((size_t)m * FF + (n0 >> 1)) * 2), pk);
+  __device__ u32x4 pack(int, f32x4 v) const {
+    return u32x4{pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]), 0u, 0u, 0u};
   }
+  __device__ uint32_t row_off(int m, int n0) const { return off + (uint32_t)(((size_t)m * FF + (n0 >> 1)) * 2); }
 };
 
 struct EpiPart : NoPre {  // fp32 partial sums [split][MP][1024]
+  static constexpr int kRowBytes = 16;
+  static constexpr bool kStaged = false;
   rsrc_t ws;
   uint32_t off;
   int MP, split;
-  __device__ void operator()(int n0, int m, f32x4 v, Pre) const {
-    st_b128(ws, off + (uint32_t)((((size_t)split * MP + m) * D + n0) * 4), as_u32x4(v));
-  }
+  __device__ u32x4 pack(int, f32x4 v) const { return as_u32x4(v); }
+  __device__ uint32_t row_off(int m, int n0) const { return off + (uint32_t)((((size_t)split * MP + m) * D + n0) * 4); }
 };
 
 // ---------------------------------------------------------------- norm rows

@@ -268,8 +268,8 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
       * stage_cycles (int64, >= 16 entries) accumulates ticks of the 100 MHz GPU clock per stage
         (``_lib.STAGE_TICK_HZ``), where the reference accumulates clock64() cycles;
       * check_status=True waits for the launch, reads the kernel status and, when it is non-zero
-        (a capped wait expired, or the XCD placement differed), re-initialises the workspace and
-        raises FlashActError.
+        (a capped wait expired, the XCD placement differed, or an exchanged partial sum left the
+        fp16 range), re-initialises the workspace and raises FlashActError.
     Rows [Tv, rows) of x_t are left untouched (the reference also integrates padded rows).
     """
     L = _lib.lib()

@@ -22,15 +22,17 @@
 //         values), then read everything and re-read any value whose parity is still stale, so no
 //         grid-wide barrier exists anywhere.
 //   (the reference runs 9 grid-wide barriers per layer: src/pi05/mk6.cu:301-497).
-//   N1/N2/FINAL: waves 0/1 of rank r own tokens r / r+32: sum the 8 XCD partials (layer 0 of a
+//   N1/N2/FINAL: rank r owns tokens r and r+32, each normed by the wave that owns its token tile
+//        (waves 0 and 2 on ranks 0-15, waves 1 and 3 on ranks 16-31), so a tile's chain of
+//        stages runs on one wave index across the XCD: sum the 8 XCD partials (layer 0 of a
 //        step: the action embedding instead), gated residual (the residual x and x_t live in
 //        LDS), adaRMS -> bf16 operand (or the final action projection and Euler update).
 //   QKV: 768 rows per XCD (q rows of head g + all k and v rows), 24 rows per CU, RoPE epilogue.
-//   ATT: head g, keys split into 32 chunks (one per rank). A chunk's first 32 keys are read
-//        from its LDS ring pages: prefix keys prefetched by the loader, this step's own keys
-//        copied in from the XCD-private copies QKV writes in the same layout. MFMA S^T = K Q^T,
-//        online softmax, O^T = V^T P^T; normalised partial O (bf16, whole operand fragments)
-//        with (m, l) per chunk.
+//   ATT: head g, prefix keys split into 32 chunks (one per rank), the first 32 of a chunk from
+//        the LDS ring pages the loader prefetched; this step's keys of tokens r and r+32 from the
+//        XCD-private copies QKV writes, as one more block. MFMA S^T = K Q^T, online softmax,
+//        O^T = V^T P^T; normalised partial O (bf16, whole operand fragments) with (m, l) per
+//        chunk.
 //   COMB: flash-decoding combine of the 32 chunk partials, one operand fragment of attn_g per
 //        rank (four waves, eight chunks each, meeting in LDS).
 //   O:   W_o[32r..32r+32, 256g..256g+256) x attn_g -> partial o_g.
@@ -91,7 +93,7 @@ static_assert(OFF_XFLAG + NX * NR * NCW * 8 <= kWsCounters, "flags stay below th
 
 // LDS layout (bytes)
 constexpr uint32_t L_CTL = RING * PAGE;        // u32 ready[2], consumed[4], abort, -, staging count, combine count
-constexpr uint32_t L_XRES = L_CTL + 64;        // f32 [2][1024] residual stream of tokens r, r+32
+constexpr uint32_t L_XRES = L_CTL + 64;        // f32 [2][1024] residual stream of tokens r, r+32 (slot = wave / 2)
 constexpr uint32_t L_XT = L_XRES + 2 * D * 4;  // f32 [2][32] x_t of tokens r, r+32
 constexpr uint32_t L_COMB = L_XT + 2 * AD * 4;  // f32 [3][64][10] combine hand-off (waves 1-3 -> 0)
 constexpr uint32_t LDS_BYTES = L_COMB + 3 * 64 * 10 * 4;
@@ -215,9 +217,9 @@ __device__ __forceinline__ void xcd_wait_ranks(const Ctx& c, int r0, int n, int 
   asm volatile("" ::: "memory");  // loads after the wait stay after it
 }
 
-// Waits for the norm waves that wrote the operand rows of this wave's token tile (token t is
-// normed by rank t % 32, wave t / 32).
-__device__ __forceinline__ void wait_norm_rows(const Ctx& c) { xcd_wait_ranks(c, 16 * (c.wave & 1), 16, c.wave >> 1); }
+// Waits for the norm waves that wrote the operand rows of this wave's token tile w (token t is
+// normed by rank t % 32, wave t / 16: ranks 16 (w % 2) .. +15, wave w).
+__device__ __forceinline__ void wait_norm_rows(const Ctx& c) { xcd_wait_ranks(c, 16 * (c.wave & 1), 16, c.wave); }
 
 // ---------------------------------------------------------------- weight ring
 // Compute wave side: wait until both loader waves have landed page pg; release pages < upto.
@@ -548,16 +550,17 @@ __device__ __forceinline__ void xread(const Ctx& c, int buf, int t, unsigned par
   stamp(c, ts);
 }
 
-// ---------------------------------------------------------------- norm stages (waves 0, 1)
+// ---------------------------------------------------------------- norm stages
 // MODE 0: x = embed(x_t) (layer 0).  MODE 1: x += gate * sum_g part_g.  MODE 2: as 1, then the
-// final norm, action projection and Euler update of x_t. Token t = r + 32*wave; lane holds
+// final norm, action projection and Euler update of x_t. Token t = r + 32 (wave / 2) (slot wave / 2
+// of the rank's LDS residual rows), run by waves whose parity is r / 16; lane holds
 // columns ncol(lane, k) + i (k, i < 4).
 template <int MODE>
 __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int buf, unsigned par, const float* gate,
                                            const float* scale, const float* shift, float dt) {
-  const int t = c.r + 32 * c.wave;
-  float* xres = reinterpret_cast<float*>(fa_lds + L_XRES) + c.wave * D;
-  float* xt = reinterpret_cast<float*>(fa_lds + L_XT) + c.wave * AD;
+  const int t = c.r + 32 * (c.wave >> 1);
+  float* xres = reinterpret_cast<float*>(fa_lds + L_XRES) + (c.wave >> 1) * D;
+  float* xt = reinterpret_cast<float*>(fa_lds + L_XT) + (c.wave >> 1) * AD;
   f32x4 sc[4], sh[4], gt[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
@@ -1184,9 +1187,9 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
     poll_flags(c.ws, OFF_XFLAG, NX * NR * NCW * 8, c.e, c.err);
   }
   const int NL = p.NL;
-  const bool nw = c.wave < 2 && c.r + 32 * c.wave < p.Tv;  // this wave owns a token in norm stages
+  const bool nw = (c.wave & 1) == (c.r >> 4) && c.r + 32 * (c.wave >> 1) < p.Tv;  // this wave owns a token in norm stages
   if (nw && c.lane < AD)
-    reinterpret_cast<float*>(fa_lds + L_XT)[c.wave * AD + c.lane] = p.x_t[(c.r + 32 * c.wave) * AD + c.lane];
+    reinterpret_cast<float*>(fa_lds + L_XT)[(c.wave >> 1) * AD + c.lane] = p.x_t[(c.r + 32 * (c.wave >> 1)) * AD + c.lane];
 
   const float dt = -1.0f / (float)p.S;
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -1268,7 +1271,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
     mark(p, c, 8, t0);
   }
   if (c.g == 0 && nw && c.lane < AD)
-    p.x_t[(c.r + 32 * c.wave) * AD + c.lane] = reinterpret_cast<float*>(fa_lds + L_XT)[c.wave * AD + c.lane];
+    p.x_t[(c.r + 32 * (c.wave >> 1)) * AD + c.lane] = reinterpret_cast<float*>(fa_lds + L_XT)[(c.wave >> 1) * AD + c.lane];
   if (blockIdx.x == 0 && c.wave == 0 && c.lane == 0) {
     __hip_atomic_store(reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 12), (xbase + (unsigned)(p.S * NL)) & 1u,
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -569,6 +569,7 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
   grid.err = reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 8);
   const uint64_t seq = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
   grid.e = seq << 32;
+  if (threadIdx.x == 0 && xcc_id() != (blockIdx.x & 7u)) atomicOr(grid.err, kErrXcd);
   if (blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_store(reinterpret_cast<unsigned*>(p.ws + kWsOwner), kOwnerMa2Generic, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);

@@ -92,7 +92,7 @@ constexpr uint32_t WS_BYTES = OFF_VS + NX * NR * 2 * HD * 2;
 static_assert(OFF_XFLAG + NX * NR * NCW * 8 <= kWsCounters, "flags stay below the fixup counters");
 
 // LDS layout (bytes)
-constexpr uint32_t L_CTL = RING * PAGE;        // u32 ready[2], consumed[4], abort, -, staging count, combine count
+constexpr uint32_t L_CTL = RING * PAGE;        // u32 ready[2], consumed[4], abort, -, -, combine count
 constexpr uint32_t L_XRES = L_CTL + 64;        // f32 [2][1024] residual stream of tokens r, r+32 (slot = wave / 2)
 constexpr uint32_t L_XT = L_XRES + 2 * D * 4;  // f32 [2][32] x_t of tokens r, r+32
 constexpr uint32_t L_COMB = L_XT + 2 * AD * 4;  // f32 [3][64][10] combine hand-off (waves 1-3 -> 0)

@@ -5,7 +5,7 @@
 //
 // Per layer (grid barrier after each stage), token m = b * Tv + t of sample b:
 //   N1   x = embed(x_t) (layer 0) or x += gate_post * sum(down partials); xn = adaRMS(x)
-//   QKV  [M x 2560] = xn W1^T; RoPE; q -> per-sample fragment-ordered Q; k, v -> the caller's
+//   QKV  [M x 2560] = xn W1^T (96-token tiles); RoPE; q -> per-sample fragment-ordered Q; k, v -> the caller's
 //        caches (row / column Lp + t of layer l), as the reference does (src/pi05/mk6.cu:307-310)
 //   ATT  per (sample, 128-key chunk, group of 16 query tiles): MQA over the chunk (8 heads x Tv
 //        query rows share the one K/V head), online softmax, normalised partial O + (m, l)
@@ -261,7 +261,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       {
         EpiQKV e{ws, kc, vc, p.rope_cos, p.rope_sin, (uint32_t)L.qf, L.NQT, p.Tv, NL, p.Lmax, p.Lp, l, 0};
         gx.W = p.w1 + (size_t)l * 2560 * D;
-        gemm_stage<4, 4>(gx, 2560, D, 1, e);
+        gemm_stage<3, 4>(gx, 2560, D, 1, e);  // 96-token tiles: 180 items fill more of the 256 CUs than 140
       }
       mark(p, 1, t0);
       grid_sync(grid);

@@ -195,12 +195,20 @@ __device__ __forceinline__ float wave_max(float v) {
   return cols_max(v);
 }
 
+// GeLU with the tanh approximation (Hendrycks & Gimpel 2016), x (1 + tanh y) / 2 with
+// y = sqrt(2/pi) (x + 0.044715 x^3), written through the identity (1 + tanh y) / 2 = 1 / (1 + e^-2y)
+// as x / (1 + 2^(-2 y log2 e)): one v_exp_f32 and one v_rcp_f32 (about 1 ulp each) and five more
+// instructions, where tanhf took about 30 with both of its branches. The tails need no care:
+// 2^t -> inf gives x * 0, 2^t -> 0 gives x. (Prefill 6.54 -> 6.18 ms, pi0.5 batch 16 21.5 -> 21.2 ms.)
 __device__ __forceinline__ float gelu_tanh(float x) {
-  // GeLU with the tanh approximation (Hendrycks & Gimpel 2016).
-  const float k0 = 0.7978845608028654f;
-  return 0.5f * x * (1.0f + tanhf(k0 * (x + 0.044715f * x * x * x)));
+  constexpr float c1 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
+  constexpr float c3 = c1 * 0.044715f;
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * (c1 + c3 * (x * x))));
 }
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+// x / (1 + e^-x) in the same form (expf and an IEEE divide took about 25 instructions).
+__device__ __forceinline__ float silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
 
 // 2^x as the bare v_exp_f32, for softmax weights and their rescale factors: a result below 2^-126
 // comes out as zero or a flushed value instead of an exact denormal (exp2f adds a range fix-up of

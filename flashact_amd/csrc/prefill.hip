@@ -13,9 +13,10 @@
 //        (the prefix attends to itself without a mask), online softmax -> partial O + (m, l)
 //   COMB combine of the key chunks -> attn [M x 2048]
 //   O    [M x 2048] = attn Wo^T, K split 2 ways -> fp32 partials
-//   N2   x += sum(partials); xn = rms(x) (1 + w_post)
-//   GU   [M x 32768] = xn Wgu^T (gate/up rows interleaved) -> h = gelu_tanh(g) u [M x 16384]
-//   DN   [M x 2048] = h Wdn^T, K split 2 ways -> fp32 partials
+//   N2   x += sum(partials); xn = rms(x) (1 + w_post), written in MFMA fragment order
+//   GU   [M x 32768] = xn Wgu^T (gate/up rows interleaved, 256 x 128 tiles) -> h = gelu_tanh(g) u
+//        [M x 16384], fragment order
+//   DN   [M x 2048] = h Wdn^T (256 x 128 tiles), K split 4 ways -> fp32 partials
 // The last layer stops after QKV: its attention and MLP outputs reach no cache entry.
 #include "engine.h"
 #include "mqa256.h"
@@ -29,7 +30,7 @@ using namespace fa::mqa;
 
 constexpr int D = 2048, FF = 16384;
 constexpr int QKVN = QD + 2 * HD;  // 2560 projection rows
-constexpr int KSPLIT = 2;          // K split of the O and down projections
+constexpr int KS_O = 2, KS_DN = 4;  // K splits of the O and down projections
 constexpr int MAX_TOKENS = 16384;  // batch x Lp
 
 struct Layout {
@@ -58,7 +59,7 @@ __host__ __device__ inline Layout layout(int B, int Lp, int Lmax) {
   L.ml = take((size_t)B * L.NKC * L.NQT * 16 * 8);
   L.attn = take((size_t)L.MP * QD * 2);
   L.h = take((size_t)L.MP * FF * 2);
-  L.part = take((size_t)KSPLIT * L.MP * D * 4);
+  L.part = take((size_t)KS_DN * L.MP * D * 4);
   L.total = o;
   return L;
 }
@@ -84,16 +85,28 @@ struct Params {
   int NL, Lp, Lmax, Tv, B;
 };
 
-struct EpiGelu : NoPre {  // rows 2f, 2f+1 = gate f, up f -> h[m][f] = gelu_tanh(g) u
-  static constexpr int kRowBytes = 4;
-  static constexpr bool kStaged = true;
+// h = gelu_tanh(g) u in MFMA fragment order (the down projection's tall-tile operand): rows 2f, 2f+1
+// of the tile are gate f, up f; the lane's features f, f + 1 (f even) of token m are 4 bytes of the
+// 16-byte slot (k-quarter (f % 32) / 8, token m % 16) of fragment (m / 16, f / 32).
+struct EpiGeluF {
   rsrc_t ws;
   uint32_t off;
   int split;
-  __device__ u32x4 pack(int, f32x4 v) const {
-    return u32x4{pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]), 0u, 0u, 0u};
+  __device__ void operator()(int n, int m, f32x4 v) const {
+    const int f = n >> 1;
+    const uint32_t o = off + (uint32_t)(((((size_t)(m >> 4) * (FF / 32) + (f >> 5)) * 64 + ((f & 31) >> 3) * 16 +
+                                          (m & 15)) * 16) + (f & 7) * 2);
+    st_b32(ws, o, pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]));
   }
-  __device__ uint32_t row_off(int m, int n0) const { return off + (uint32_t)(((size_t)m * FF + (n0 >> 1)) * 2); }
+};
+
+struct EpiPartT {  // fp32 partial sums [split][MP][2048] from the tall tile: 16 bytes per lane and block
+  rsrc_t ws;
+  uint32_t off;
+  int MP, split;
+  __device__ void operator()(int n, int m, f32x4 v) const {
+    st_b128(ws, off + (uint32_t)((((size_t)split * MP + m) * D + n) * 4), as_u32x4(v));
+  }
 };
 
 struct EpiPart : NoPre {  // fp32 partial sums [split][MP][2048]
@@ -107,8 +120,10 @@ struct EpiPart : NoPre {  // fp32 partial sums [split][MP][2048]
 };
 
 // One wave per token row; lane holds columns 4 lane + 256 k + i (k < 8). FIRST: x = the prefix
-// hidden states; otherwise x += the sum of the K-split partials. Then xn = rms(x) (1 + w).
-template <bool FIRST>
+// hidden states; otherwise x += the sum of the NS K-split partials. Then xn = rms(x) (1 + w), row-major
+// [M][2048] for the QKV tile, or with FRAG in MFMA fragment order for the gate/up tall tile (column d
+// of token m: 8 bytes of the slot (k-quarter (d % 32) / 8, token m % 16) of fragment (m / 16, d / 32)).
+template <bool FIRST, int NS, bool FRAG>
 __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xin, const float* w) {
   const Layout& L = p.L;
   const int lane = lane_id();
@@ -120,20 +135,20 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xi
       for (int k = 0; k < 8; k++)
         x[k] = as_f32x4(ldb128<kCpPlain>(xin, (uint32_t)(((size_t)m * D + 4 * lane + 256 * k) * 4)));
     } else {
-      u32x4 xo[8], pr[KSPLIT][8];
+      u32x4 xo[8], pr[NS][8];
 #pragma unroll
       for (int k = 0; k < 8; k++) {
         const int d = 4 * lane + 256 * k;
         xo[k] = ldb128<kCpSc1>(ws, (uint32_t)(L.x + ((size_t)m * D + d) * 4));
 #pragma unroll
-        for (int s = 0; s < KSPLIT; s++)
+        for (int s = 0; s < NS; s++)
           pr[s][k] = ldb128<kCpSc1>(ws, (uint32_t)(L.part + (((size_t)s * L.MP + m) * D + d) * 4));
       }
 #pragma unroll
       for (int k = 0; k < 8; k++) {
         f32x4 s = as_f32x4(pr[0][k]);
 #pragma unroll
-        for (int sp = 1; sp < KSPLIT; sp++) s += as_f32x4(pr[sp][k]);
+        for (int sp = 1; sp < NS; sp++) s += as_f32x4(pr[sp][k]);
         x[k] = as_f32x4(xo[k]) + s;
       }
     }
@@ -149,12 +164,16 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xi
 #pragma unroll
       for (int i = 0; i < 4; i++) h[i] = x[k][i] * rr * (1.0f + wv[i]);
       st_b128(ws, (uint32_t)(L.x + ((size_t)m * D + d) * 4), as_u32x4(x[k]));
-      st_b64(ws, (uint32_t)(L.xn + ((size_t)m * D + d) * 2), u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])});
+      const uint32_t xa = FRAG ? (uint32_t)((((size_t)(m >> 4) * (D / 32) + (d >> 5)) * 64 + ((d & 31) >> 3) * 16 +
+                                               (m & 15)) * 16 + (d & 7) * 2)
+                                : (uint32_t)(((size_t)m * D + d) * 2);
+      st_b64(ws, (uint32_t)L.xn + xa, u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])});
     }
   }
 }
 
-constexpr uint32_t LDS_BYTES = GemmShape<4, 4>::LDS > ATT_LDS ? GemmShape<4, 4>::LDS : ATT_LDS;
+constexpr uint32_t LDS_GEMM = GemmShape<4, 4>::LDS > TALL_LDS ? GemmShape<4, 4>::LDS : TALL_LDS;
+constexpr uint32_t LDS_BYTES = LDS_GEMM > ATT_LDS ? LDS_GEMM : ATT_LDS;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {
@@ -184,13 +203,15 @@ __global__ void __launch_bounds__(NTHR, 1) prefill_kernel(Params p) {
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   GemmArgs gx{reinterpret_cast<const bf16*>(p.ws + L.xn), nullptr, D, D, L.M};
   GemmArgs ga{reinterpret_cast<const bf16*>(p.ws + L.attn), nullptr, QD, QD, L.M};
-  GemmArgs gh{reinterpret_cast<const bf16*>(p.ws + L.h), nullptr, FF, FF, L.M};
+  const uint32_t mb16 = (uint32_t)((L.M + 15) / 16 * 16);  // tokens of the fragment-ordered operands
+  GemmArgsF gxf{make_rsrc(p.ws + L.xn, mb16 * D * 2), nullptr, D / 32, D, L.M};
+  GemmArgsF ghf{make_rsrc(p.ws + L.h, mb16 * FF * 2), nullptr, FF / 32, FF, L.M};
 #pragma unroll 1
   for (int l = 0; l < NL; l++) {
     if (l == 0)
-      stage_norm<true>(p, ws, xin, p.ln_in);
+      stage_norm<true, 1, false>(p, ws, xin, p.ln_in);
     else
-      stage_norm<false>(p, ws, xin, p.ln_in + (size_t)l * D);
+      stage_norm<false, KS_DN, false>(p, ws, xin, p.ln_in + (size_t)l * D);
     mark(p, 0, t0);
     grid_sync(grid);
     mark(p, 9, t0);
@@ -214,27 +235,27 @@ __global__ void __launch_bounds__(NTHR, 1) prefill_kernel(Params p) {
     {
       EpiPart e{{}, ws, (uint32_t)L.part, L.MP, 0};
       ga.W = p.wo + (size_t)l * D * QD;
-      gemm_stage<4, 4>(ga, D, QD, KSPLIT, e);
+      gemm_stage<4, 4>(ga, D, QD, KS_O, e);
     }
     mark(p, 4, t0);
     grid_sync(grid);
     mark(p, 9, t0);
-    stage_norm<false>(p, ws, xin, p.ln_post + (size_t)l * D);
+    stage_norm<false, KS_O, true>(p, ws, xin, p.ln_post + (size_t)l * D);
     mark(p, 5, t0);
     grid_sync(grid);
     mark(p, 9, t0);
     {
-      EpiGelu e{{}, ws, (uint32_t)L.h, 0};
-      gx.W = p.wgu + (size_t)l * 2 * FF * D;
-      gemm_stage<4, 4>(gx, 2 * FF, D, 1, e);
+      EpiGeluF e{ws, (uint32_t)L.h, 0};
+      gxf.W = p.wgu + (size_t)l * 2 * FF * D;
+      gemm_stage_tall(gxf, 2 * FF, D, 1, e);
     }
     mark(p, 6, t0);
     grid_sync(grid);
     mark(p, 9, t0);
     {
-      EpiPart e{{}, ws, (uint32_t)L.part, L.MP, 0};
-      gh.W = p.wdn + (size_t)l * D * FF;
-      gemm_stage<4, 4>(gh, D, FF, KSPLIT, e);
+      EpiPartT e{ws, (uint32_t)L.part, L.MP, 0};
+      ghf.W = p.wdn + (size_t)l * D * FF;
+      gemm_stage_tall(ghf, D, FF, KS_DN, e);
     }
     mark(p, 7, t0);
     grid_sync(grid);

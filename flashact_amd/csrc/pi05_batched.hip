@@ -11,10 +11,11 @@
 //        query rows share the one K/V head), online softmax, normalised partial O + (m, l)
 //   COMB flash-decoding combine of the key chunks -> attn [M x 2048]
 //   O    [M x 1024] = attn Wo^T, K split 4 ways -> fp32 partials
-//   N2   x += gate_in * sum(partials); xn = adaRMS(x)
-//   GU   [M x 8192] = xn W2^T (gate/up rows interleaved) -> h = gelu_tanh(g) u [M x 4096]
-// (all GEMMs: 128-token x 128-row tiles, k steps of 128)
+//   N2   x += gate_in * sum(partials); xn = adaRMS(x), written in MFMA fragment order
+//   GU   [M x 8192] = xn W2^T (gate/up rows interleaved; 256-token tall tiles) -> h = gelu_tanh(g) u
+//        [M x 4096]
 //   DN   [M x 1024] = h W3^T, K split 4 ways -> fp32 partials
+// (GEMMs other than GU: 128-row weight tiles of 128 tokens, 96 for QKV; k steps of 128)
 // then the final norm, action projection and Euler update (src/pi05/mk6.cu:502-517).
 #include "engine.h"
 #include "mqa256.h"
@@ -84,16 +85,15 @@ struct Params {
   int NL, Lp, Lmax, S, Tv, B, xt_rows;
 };
 
-struct EpiGelu : NoPre {  // rows 2f, 2f+1 = gate f, up f -> h[m][f] = gelu_tanh(g) u
-  static constexpr int kRowBytes = 4;
-  static constexpr bool kStaged = false;
+// The tall tile's gate/up epilogue: rows 2f, 2f+1 = gate f, up f -> h[m][f] = gelu_tanh(g) u (row-major,
+// the down projection's 128-token tiles copy it by rows).
+struct EpiGeluT {
   rsrc_t ws;
   uint32_t off;
   int split;
-  __device__ u32x4 pack(int, f32x4 v) const {
-    return u32x4{pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]), 0u, 0u, 0u};
+  __device__ void operator()(int n, int m, f32x4 v) const {
+    st_b32(ws, off + (uint32_t)(((size_t)m * FF + (n >> 1)) * 2), pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]));
   }
-  __device__ uint32_t row_off(int m, int n0) const { return off + (uint32_t)(((size_t)m * FF + (n0 >> 1)) * 2); }
 };
 
 struct EpiPart : NoPre {  // fp32 partial sums [split][MP][1024]
@@ -109,8 +109,10 @@ struct EpiPart : NoPre {  // fp32 partial sums [split][MP][1024]
 // ---------------------------------------------------------------- norm rows
 // One wave per token row; lane holds columns 4 lane + 256 k + i. MODE 0: x = embed(x_t);
 // MODE 1: x += gate * sum of the K-split partials; MODE 2: as 1, then final norm + action
-// projection + Euler update of x_t.
-template <int MODE>
+// projection + Euler update of x_t. xn is row-major [M][1024] for the 128-token tiles, or with FRAG in
+// MFMA fragment order for the tall tile (column d of token m: 8 bytes of the slot (k-quarter
+// (d % 32) / 8, token m % 16) of fragment (m / 16, d / 32)).
+template <int MODE, bool FRAG = false>
 __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xtr, const float* gate, const float* scale, const float* shift,
                            float dt) {
   const Layout& L = p.L;
@@ -180,8 +182,10 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
       for (int k = 0; k < 4; k++) {
         const int d = 4 * lane + 256 * k;
         st_b128(ws, (uint32_t)(L.x + ((size_t)m * D + d) * 4), as_u32x4(x[k]));
-        st_b64(ws, (uint32_t)(L.xn + ((size_t)m * D + d) * 2),
-               u32x2{pack_bf16x2(h[k][0], h[k][1]), pack_bf16x2(h[k][2], h[k][3])});
+        const uint32_t xa = FRAG ? (uint32_t)((((size_t)(m >> 4) * (D / 32) + (d >> 5)) * 64 + ((d & 31) >> 3) * 16 +
+                                                (m & 15)) * 16 + (d & 7) * 2)
+                                 : (uint32_t)(((size_t)m * D + d) * 2);
+        st_b64(ws, (uint32_t)L.xn + xa, u32x2{pack_bf16x2(h[k][0], h[k][1]), pack_bf16x2(h[k][2], h[k][3])});
       }
     } else {
       float acc = 0.f;  // lane a < 32 ends with v[a]
@@ -212,7 +216,8 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
 }
 
 // ---------------------------------------------------------------- the kernel
-constexpr uint32_t LDS_BYTES = GemmShape<4, 4>::LDS > ATT_LDS ? GemmShape<4, 4>::LDS : ATT_LDS;
+constexpr uint32_t LDS_GEMM = GemmShape<4, 4>::LDS > TALL_LDS ? GemmShape<4, 4>::LDS : TALL_LDS;
+constexpr uint32_t LDS_BYTES = LDS_GEMM > ATT_LDS ? LDS_GEMM : ATT_LDS;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {
@@ -244,6 +249,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
   GemmArgs gx{reinterpret_cast<const bf16*>(p.ws + L.xn), nullptr, D, D, L.M};
   GemmArgs ga{reinterpret_cast<const bf16*>(p.ws + L.attn), nullptr, QD, QD, L.M};
   GemmArgs gh{reinterpret_cast<const bf16*>(p.ws + L.h), nullptr, FF, FF, L.M};
+  GemmArgsF gxf{make_rsrc(p.ws + L.xn, (uint32_t)((L.M + 15) / 16 * 16) * D * 2), nullptr, D / 32, D, L.M};
 #pragma unroll 1
   for (int step = 0; step < p.S; step++) {
 #pragma unroll 1
@@ -282,14 +288,14 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       mark(p, 4, t0);
       grid_sync(grid);
       mark(p, 9, t0);
-      stage_norm<1>(p, ws, xtr, mod_in + 2 * D, mod_post, mod_post + D, 0.f);
+      stage_norm<1, true>(p, ws, xtr, mod_in + 2 * D, mod_post, mod_post + D, 0.f);
       mark(p, 5, t0);
       grid_sync(grid);
       mark(p, 9, t0);
       {
-        EpiGelu e{{}, ws, (uint32_t)L.h, 0};
-        gx.W = p.w2 + (size_t)l * 8192 * D;
-        gemm_stage<4, 4>(gx, 8192, D, 1, e);
+        EpiGeluT e{ws, (uint32_t)L.h, 0};
+        gxf.W = p.w2 + (size_t)l * 8192 * D;
+        gemm_stage_tall(gxf, 8192, D, 1, e);
       }
       mark(p, 6, t0);
       grid_sync(grid);

@@ -9,6 +9,8 @@
 // with sc1 (buffer loads, or global_load_lds ... sc1 for GEMM operands); weights and the prefix
 // K/V are read-only inputs.
 #pragma once
+#include <type_traits>
+
 #include "fa_device.h"
 
 namespace fa {
@@ -143,6 +145,10 @@ __device__ __forceinline__ void grid_sync(Grid& g) {
 // LDS pitch 1040 B. An MFMA fragment (16 rows of one 16-row block, 32 k) then reads row r from
 // copy r at 1040 r + 256 (block % 4) + 64 ks + 16 q: the 16 rows fall in 16 different bank groups.
 // Two-step ring, one workgroup barrier per step. Rows m >= M copy row 0 (results discarded).
+// With AF the activations are in MFMA fragment order instead (fragment (token block tb, k-step kk) =
+// 1 KB at (tb lda / 32 + kk) * 1024, lane l = lr + 16 q holding token lr, k 8q..8q+7 at 16 l): copy f
+// of a step is fragment (token block f / 4, k-step f % 4), one contiguous 1 KB, and lands whole in slot
+// f, where the lane's operand is simply its own 16 bytes.
 struct GemmArgs {
   const bf16* A;  // [M][lda] activations (written in this launch: sc1 copies)
   const bf16* W;  // [N][ldw] weights
@@ -161,7 +167,7 @@ struct GemmShape {
   static_assert(BN % 64 == 0, "weight tiles are whole 64-row groups");
 };
 
-template <int WM, int WN, class Epi>
+template <int WM, int WN, bool AF = false, class Epi>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int k0, int k1, Epi& epi) {
   using S = GemmShape<WM, WN>;
   const int w = wave_id(), lane = lane_id(), lr = lane & 15, lq = lane >> 4;
@@ -172,9 +178,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
   for (int j = 0; j < S::IPW; j++) {
     const int f = w + 4 * j;
     if (f < 16 * S::GA) {
-      int row = m0 + 64 * (f >> 4) + 16 * lq + (f & 15);
-      if (row >= g.M || 64 * (f >> 4) + 16 * lq >= S::BM) row = 0;
-      src[j] = reinterpret_cast<const unsigned char*>(g.A + (size_t)row * g.lda + k0 + 8 * lr);
+      if constexpr (AF) {
+        // blocks past the tile or past M copy the last token block of the operand (results discarded)
+        int tb = (m0 >> 4) + (f >> 2);
+        if (16 * (f >> 2) >= S::BM || 16 * tb >= g.M) tb = (g.M - 1) >> 4;
+        src[j] = reinterpret_cast<const unsigned char*>(g.A) + ((size_t)tb * (g.lda >> 5) + (k0 >> 5) + (f & 3)) * 1024 +
+                 16 * lane;
+      } else {
+        int row = m0 + 64 * (f >> 4) + 16 * lq + (f & 15);
+        if (row >= g.M || 64 * (f >> 4) + 16 * lq >= S::BM) row = 0;
+        src[j] = reinterpret_cast<const unsigned char*>(g.A + (size_t)row * g.lda + k0 + 8 * lr);
+      }
     } else {
       const int fw = f - 16 * S::GA;
       const int row = n0 + 64 * (fw >> 4) + 16 * lq + (fw & 15);
@@ -188,7 +202,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
     for (int j = 0; j < S::IPW; j++) {
       const int f = w + 4 * j;
       if (f < 16 * S::GA)
-        dma16<true>(src[j] + 256 * s, lds_addr(base + f * S::PITCH));
+        dma16<true>(src[j] + (AF ? 4096 : 256) * s, lds_addr(base + f * S::PITCH));
       else
         dma16<false>(src[j] + 256 * s, lds_addr(base + f * S::PITCH));
     }
@@ -212,7 +226,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
 #pragma unroll
       for (int i = 0; i < WM; i++) {
         const int mb = wm * WM + i;  // 16-row block of A
-        a[h][i] = lds128(base + (16 * (mb >> 2) + lr) * S::PITCH + (mb & 3) * 256 + ks * 64 + lq * 16);
+        a[h][i] = AF ? lds128(base + (mb * 4 + ks) * S::PITCH + 16 * lane)
+                     : lds128(base + (16 * (mb >> 2) + lr) * S::PITCH + (mb & 3) * 256 + ks * 64 + lq * 16);
       }
 #pragma unroll
       for (int j = 0; j < WN; j++) {
@@ -317,7 +332,7 @@ struct NoPre {
 // Runs every tile of an [M x N] GEMM, K split into `ksplit` equal ranges (multiples of 128). Items
 // are ordered m-tile fastest so the items of one weight tile run on neighbouring CUs of one XCD.
 // The epilogue receives the split index through epi.split.
-template <int WM, int WN, class Epi>
+template <int WM, int WN, bool AF = false, class Epi>
 __device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int ksplit, Epi& epi) {
   using S = GemmShape<WM, WN>;
   const int nm = (g.M + S::BM - 1) / S::BM, nn = N / S::BN;
@@ -326,25 +341,31 @@ __device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int 
   for (int it = vwg(); it < items; it += NWG) {
     const int mt = it % nm, rest = it / nm, nt = rest % nn, sp = rest / nn;
     epi.split = sp;
-    gemm_tile<WM, WN>(g, mt * S::BM, nt * S::BN, sp * kc, sp * kc + kc, epi);
+    gemm_tile<WM, WN, AF>(g, mt * S::BM, nt * S::BN, sp * kc, sp * kc + kc, epi);
   }
 }
 
-// ---------------------------------------------------------------- tall GEMM tile (256 x 128)
-// For GEMMs with many output tiles. The 4 waves are stacked along the tokens: wave w computes tokens
-// 64w..64w+63 of the tile against all 128 weight rows (4 x 8 MFMA blocks, 32 MFMAs per 32-k sub-step
-// for 12 fragment reads, against 16 for 8 in gemm_tile). Each token fragment is used by one wave
-// only, so the activations skip LDS: they are stored in MFMA fragment order (fragment (token block
-// tb, k-step kk) = 1 KB at (tb KF + kk) * 1024, lane l = lr + 16 q holding token lr, k 8q..8q+7 at
-// 16 l) and loaded straight into registers, a whole 128-k step ahead of their use. The weights go
-// through a 4-stage LDS ring (the 4-row x 256 B copies of gemm_tile) filled three steps ahead. The
-// loads of later steps are issued between the MFMAs instead of in one burst before them, which at one
-// wave per SIMD would stall the MFMA issue behind the copy queue: the weight copies during sub-steps
-// 0-1, and after each sub-step the next step's four activation fragments of that sub-step, into the
-// registers its MFMAs have just read (one activation register set: 64 VGPRs, which keeps the
-// persistent kernels free of spills). Measured in isolation on L2-resident operands (`_work` probe,
-// 256 CUs): 7.5 µs per 128 x 128 x 1024 of work against 10.2-10.6 µs for gemm_tile; in the prefill
-// kernel, gate/up 181 -> 133 µs and down 86 -> 73 µs per layer.
+// ---------------------------------------------------------------- direct-operand GEMM tiles
+// gemm_tile_d<TW, WM>: a (16 WM TW)-token x 128-feature tile whose token operand skips LDS. The 4 waves
+// form TW rows along the tokens and 4 / TW columns along the features; wave (wt, wf) computes WM token
+// blocks x WN = 2 TW feature blocks of 16 x 16. The tall tile (TW = 4, WM = 4: 256 x 128, a wave
+// holds 64 tokens x 128 features, 32 MFMAs per 32-k sub-step for 12 fragment reads, against 16 for 8
+// in gemm_tile) is for GEMMs with many output tiles; the square one (TW = 2: 128 or 96 x 128, the
+// shape of gemm_tile) for the rest.
+// * Activations are stored in MFMA fragment order (fragment (token block tb, k-step kk) = 1 KB at
+//   (tb KF + kk) * 1024, lane l = lr + 16 q holding token lr, k 8q..8q+7 at 16 l) and loaded straight
+//   into registers, a whole 128-k step ahead of their use (the waves of one token row load the same
+//   fragments; each is used by one wave of the tall tile).
+// * The weights go through a 4-stage LDS ring (the 4-row x 256 B copies of gemm_tile) filled three
+//   steps ahead.
+// * The loads of later steps are issued between the MFMAs instead of in one burst before them, which
+//   at one wave per SIMD would stall the MFMA issue behind the copy queue: the weight copies during
+//   sub-steps 0-1, and after each sub-step the next step's WM activation fragments of that sub-step,
+//   into the registers its MFMAs have just read (one activation register set: 16 WM VGPRs, which keeps
+//   the persistent kernels free of spills; two sets spilled 32-60 VGPRs in the prefill).
+// Measured in isolation on L2-resident operands (`_work` probe, 256 CUs): the tall tile 7.5 µs per
+// 128 x 128 x 1024 of work against 10.2-10.6 µs for gemm_tile; in the prefill kernel, gate/up
+// 181 -> 133 µs and down 86 -> 73 µs per layer.
 struct GemmArgsF {
   rsrc_t A;        // fragment-ordered activations, bounded to ceil(M / 16) token blocks (loads past: 0)
   const bf16* W;   // [N][ldw] weights
@@ -353,10 +374,19 @@ struct GemmArgsF {
 constexpr uint32_t TALL_ST = 32 * 1040;   // one weight stage: 32 copies of 4 rows x 256 B
 constexpr uint32_t TALL_LDS = 4 * TALL_ST;
 
-// Epi(n, m, v): features n..n+3 of token m (m < M only).
-template <class Epi>
-__device__ __forceinline__ void gemm_tile_tall(const GemmArgsF& g, int m0, int n0, int k0, int k1, Epi& epi) {
+template <class E, class = void>
+struct HasPre : std::false_type {};
+template <class E>
+struct HasPre<E, std::void_t<typename E::Pre>> : std::true_type {};
+
+// Epilogue: epi(n, m, v) with features n..n+3 of token m (m < M only); an epilogue with a Pre type
+// (gemm_tile's interface) gets epi(n, m, v, pre) with every block's pre fetched before the first call.
+template <int TW, int WM, class Epi>
+__device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, int k0, int k1, Epi& epi) {
+  static_assert(TW == 4 || TW == 2, "4 or 2 waves along the tokens");
+  constexpr int FW = 4 / TW, WN = 8 / FW, NA = 4 * WM;
   const int w = wave_id(), lane = lane_id(), lr = lane & 15, lq = lane >> 4;
+  const int wt = w / FW, wf = w % FW;
   // copy f = w + 4 j of a step: rows 64 (f / 16) + 16 lq + f % 16 of the tile, 16 B per lane
   // (readfirstlane returns int: each half is cast to uint32_t before widening, or a low word with
   // bit 31 set would sign-extend over the high word)
@@ -365,15 +395,15 @@ __device__ __forceinline__ void gemm_tile_tall(const GemmArgsF& g, int m0, int n
   const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wb >> 32));
   const void* wbase = reinterpret_cast<const void*>(((uint64_t)whi << 32) | wlo);
   const uint32_t wlane = (uint32_t)((16 * lq * g.ldw + k0 + 8 * lr) * 2);
-  const int tb0 = (m0 >> 4) + 4 * w;  // the wave's first token block
+  const int tb0 = (m0 >> 4) + WM * wt;  // the wave's first token block
   const uint32_t abase = (uint32_t)(((size_t)tb0 * g.KF + (k0 >> 5)) * 1024 + lane * 16);
   const int ns = (k1 - k0) >> 7;
-  f32x4 acc[8][4];
+  f32x4 acc[WN][WM];
 #pragma unroll
-  for (int j = 0; j < 8; j++)
+  for (int j = 0; j < WN; j++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  u32x4 a[16];  // [4 ks + i]: token block tb0 + i, k-step ks of the current 128-k step
+    for (int i = 0; i < WM; i++) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 a[NA];  // [WM ks + i]: token block tb0 + i, k-step ks of the current 128-k step
   auto issue_w = [&](int s, int j) {
     const int f = w + 4 * j;
     dma16s(wbase, wlane + (uint32_t)((64 * (f >> 4) + (f & 15)) * g.ldw * 2 + 256 * s),
@@ -382,7 +412,7 @@ __device__ __forceinline__ void gemm_tile_tall(const GemmArgsF& g, int m0, int n
   // Token blocks past M read zeros (the descriptor's bound) and their MFMAs run on them: no branch
   // in the loop, whose basic blocks the compiler would otherwise split at every load and MFMA group.
   auto load_a = [&](int s, int q) {
-    a[q] = ldb128<kCpSc1>(g.A, abase + (uint32_t)(((q & 3) * g.KF + 4 * s + (q >> 2)) * 1024));
+    a[q] = ldb128<kCpSc1>(g.A, abase + (uint32_t)(((q % WM) * g.KF + 4 * s + q / WM) * 1024));
   };
   __builtin_amdgcn_s_waitcnt(0);  // earlier stores / loads of this wave are complete
 #pragma unroll
@@ -391,68 +421,94 @@ __device__ __forceinline__ void gemm_tile_tall(const GemmArgsF& g, int m0, int n
 #pragma unroll
       for (int j = 0; j < 8; j++) issue_w(s, j);
 #pragma unroll
-  for (int q = 0; q < 16; q++) load_a(0, q);
+  for (int q = 0; q < NA; q++) load_a(0, q);
   vm_wait<0>();
   __syncthreads();
   // One 128-k step on ring stage s % 4. The weight copies of step s + 3 go out during sub-steps 0-1;
-  // once sub-step ks's MFMAs have read their four activation fragments, the same registers take the
+  // once sub-step ks's MFMAs have read their WM activation fragments, the same registers take the
   // next step's fragments of sub-step ks (a whole step ahead of their use).
 #pragma unroll 1
   for (int s = 0; s < ns; s++) {
     const uint32_t base = (uint32_t)(s & 3) * TALL_ST;
     // one fragment register set: fragment j of sub-step ks + 1 is read right after the MFMAs that
-    // used fragment j of sub-step ks, 28 MFMAs before it is needed
-    u32x4 wf[8];
-    auto rd = [&](int ks, int j) { return lds128(base + (16 * (j >> 2) + lr) * 1040 + (j & 3) * 256 + ks * 64 + lq * 16); };
+    // used fragment j of sub-step ks
+    u32x4 wfr[WN];
+    auto rd = [&](int ks, int j) {
+      const int nb = wf * WN + j;  // 16-row feature block of the tile
+      return lds128(base + (16 * (nb >> 2) + lr) * 1040 + (nb & 3) * 256 + ks * 64 + lq * 16);
+    };
 #pragma unroll
-    for (int j = 0; j < 8; j++) wf[j] = rd(0, j);
+    for (int j = 0; j < WN; j++) wfr[j] = rd(0, j);
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        if (ks < 2 && (j & 1) == 0 && s + 3 < ns) issue_w(s + 3, 4 * ks + (j >> 1));
+      for (int j = 0; j < WN; j++) {
+        if (ks < 2 && j % (WN / 4) == 0 && s + 3 < ns) issue_w(s + 3, 4 * ks + j / (WN / 4));
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[j][i] = mfma16(wf[j], a[4 * ks + i], acc[j][i]);
-        if (ks + 1 < 4) wf[j] = rd(ks + 1, j);
+        for (int i = 0; i < WM; i++) acc[j][i] = mfma16(wfr[j], a[WM * ks + i], acc[j][i]);
+        if (ks + 1 < 4) wfr[j] = rd(ks + 1, j);
       }
       if (s + 1 < ns)
 #pragma unroll
-        for (int i = 0; i < 4; i++) load_a(s + 1, 4 * ks + i);
+        for (int i = 0; i < WM; i++) load_a(s + 1, WM * ks + i);
       __builtin_amdgcn_sched_barrier(0);
     }
     // Everything but this step's loads has landed: stage (s + 1) % 4 (copied two steps ago) for this
     // wave; the barrier makes it every wave's and frees stage s % 4.
     if (s + 3 < ns)
-      vm_wait<24>();
+      vm_wait<8 + NA>();
     else if (s + 1 < ns)
-      vm_wait<16>();
+      vm_wait<NA>();
     else
       vm_wait<0>();
     __syncthreads();
   }
-  if (16 * tb0 < g.M) {
+  if (16 * tb0 >= g.M) return;
+  if constexpr (HasPre<Epi>::value) {
+    typename Epi::Pre pre[WN][WM];
 #pragma unroll
-    for (int j = 0; j < 8; j++)
+    for (int j = 0; j < WN; j++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = m0 + 64 * w + 16 * i + lr;
-        if (m < g.M) epi(n0 + 16 * j + 4 * lq, m, acc[j][i]);
+      for (int i = 0; i < WM; i++) {
+        const int m = m0 + 16 * (WM * wt + i) + lr;
+        pre[j][i] = epi.pre(n0 + 16 * (wf * WN + j) + 4 * lq, m < g.M ? m : 0);
+      }
+#pragma unroll
+    for (int j = 0; j < WN; j++)
+#pragma unroll
+      for (int i = 0; i < WM; i++) {
+        const int m = m0 + 16 * (WM * wt + i) + lr;
+        if (m < g.M) epi(n0 + 16 * (wf * WN + j) + 4 * lq, m, acc[j][i], pre[j][i]);
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < WN; j++)
+#pragma unroll
+      for (int i = 0; i < WM; i++) {
+        const int m = m0 + 16 * (WM * wt + i) + lr;
+        if (m < g.M) epi(n0 + 16 * (wf * WN + j) + 4 * lq, m, acc[j][i]);
       }
   }
 }
 
-// Every 256 x 128 tile of an [M x N] GEMM (N a multiple of 128), K split into `ksplit` ranges
+// Every (16 WM TW) x 128 tile of an [M x N] GEMM (N a multiple of 128), K split into `ksplit` ranges
 // (multiples of 128); items m-tile fastest, as in gemm_stage. The epilogue gets the split in epi.split.
-template <class Epi>
-__device__ __forceinline__ void gemm_stage_tall(const GemmArgsF& g, int N, int K, int ksplit, Epi& epi) {
-  const int nm = (g.M + 255) / 256, nn = N / 128;
+template <int TW, int WM, class Epi>
+__device__ __forceinline__ void gemm_stage_d(const GemmArgsF& g, int N, int K, int ksplit, Epi& epi) {
+  constexpr int BM = 16 * WM * TW;
+  const int nm = (g.M + BM - 1) / BM, nn = N / 128;
   const int items = nm * nn * ksplit, kc = K / ksplit;
 #pragma unroll 1
   for (int it = vwg(); it < items; it += NWG) {
     const int mt = it % nm, rest = it / nm, nt = rest % nn, sp = rest / nn;
     epi.split = sp;
-    gemm_tile_tall(g, mt * 256, nt * 128, sp * kc, sp * kc + kc, epi);
+    gemm_tile_d<TW, WM>(g, mt * BM, nt * 128, sp * kc, sp * kc + kc, epi);
   }
+}
+
+template <class Epi>
+__device__ __forceinline__ void gemm_stage_tall(const GemmArgsF& g, int N, int K, int ksplit, Epi& epi) {
+  gemm_stage_d<4, 4>(g, N, K, ksplit, epi);
 }
 
 // Split-K GEMM whose K-splits are summed inside the stage (for small tiles: one workgroup reads the

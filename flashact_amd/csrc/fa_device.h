@@ -151,6 +151,10 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
   return as_f32((unsigned)__builtin_amdgcn_update_dpp(0, (int)as_u32(v), CTRL, 0xF, 0xF, false));
 }
+// lane l gets the value of lane l ^ 1 (DPP quad_perm [1, 0, 3, 2])
+__device__ __forceinline__ unsigned swap_adj(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+}
 struct LanePair {
   unsigned lo, hi;
 };

@@ -280,7 +280,9 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
 // ---------------------------------------------------------------- combine
 // attn[b Tv + t][256 h + d] = sum_c w_c O_c with w_c = l_c 2^(m_c - M) / sum. A wave combines 4
 // query rows at once (16 lanes per row, 16 dims per lane); the (m, l) pairs and the partials of up
-// to 8 chunks are all in flight together.
+// to 8 chunks are all in flight together. attn is stored in MFMA fragment order (the O projection's
+// token operand): the lane's 8 dims c..c+7 (c % 8 = 0) of token m are the 16-byte slot
+// (k-quarter (c % 32) / 8, token m % 16) of fragment (m / 16, c / 32).
 template <class P>
 __device__ __forceinline__ void stage_comb(const P& p, rsrc_t ws) {
   const auto& L = p.L;
@@ -343,7 +345,8 @@ __device__ __forceinline__ void stage_comb(const P& p, rsrc_t ws) {
         const u32x4 o = {pack_bf16x2(acc[e][0] * inv, acc[e][1] * inv), pack_bf16x2(acc[e][2] * inv, acc[e][3] * inv),
                          pack_bf16x2(acc[2 + e][0] * inv, acc[2 + e][1] * inv),
                          pack_bf16x2(acc[2 + e][2] * inv, acc[2 + e][3] * inv)};
-        st_b128(ws, (uint32_t)(L.attn + ((size_t)m * QD + h * HD + 32 * dp + 16 * e + 8 * jh) * 2), o);
+        const int c = h * HD + 32 * dp + 16 * e + 8 * jh;
+        st_b128(ws, (uint32_t)(L.attn + ((((size_t)(m >> 4) * (QD / 32) + (c >> 5)) * 64 + ((c & 31) >> 3) * 16 + (m & 15)) * 16)), o);
       }
     }
   }

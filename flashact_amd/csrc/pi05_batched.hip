@@ -11,11 +11,12 @@
 //        query rows share the one K/V head), online softmax, normalised partial O + (m, l)
 //   COMB flash-decoding combine of the key chunks -> attn [M x 2048]
 //   O    [M x 1024] = attn Wo^T, K split 4 ways -> fp32 partials
-//   N2   x += gate_in * sum(partials); xn = adaRMS(x), written in MFMA fragment order
-//   GU   [M x 8192] = xn W2^T (gate/up rows interleaved; 256-token tall tiles) -> h = gelu_tanh(g) u
+//   N2   x += gate_in * sum(partials); xn = adaRMS(x)
+//   GU   [M x 8192] = xn W2^T (gate/up rows interleaved; 256 x 128 tall tiles) -> h = gelu_tanh(g) u
 //        [M x 4096]
 //   DN   [M x 1024] = h W3^T, K split 4 ways -> fp32 partials
-// (GEMMs other than GU: 128-row weight tiles of 128 tokens, 96 for QKV; k steps of 128)
+// (GEMMs other than GU: 128-row weight tiles of 128 tokens, 96 for QKV, in engine.h gemm_tile.) Every
+// GEMM reads its token operand (xn, attn, h) in MFMA fragment order.
 // then the final norm, action projection and Euler update (src/pi05/mk6.cu:502-517).
 #include "engine.h"
 #include "mqa256.h"
@@ -85,14 +86,18 @@ struct Params {
   int NL, Lp, Lmax, S, Tv, B, xt_rows;
 };
 
-// The tall tile's gate/up epilogue: rows 2f, 2f+1 = gate f, up f -> h[m][f] = gelu_tanh(g) u (row-major,
-// the down projection's 128-token tiles copy it by rows).
-struct EpiGeluT {
+// Gate/up epilogue: rows 2f, 2f+1 of the tile are gate f, up f -> h = gelu_tanh(g) u in MFMA fragment
+// order (the down projection's token operand): the lane's features f, f + 1 (f even) of token m are
+// 4 bytes of the 16-byte slot (k-quarter (f % 32) / 8, token m % 16) of fragment (m / 16, f / 32).
+struct EpiGeluF {
   rsrc_t ws;
   uint32_t off;
   int split;
   __device__ void operator()(int n, int m, f32x4 v) const {
-    st_b32(ws, off + (uint32_t)(((size_t)m * FF + (n >> 1)) * 2), pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]));
+    const int f = n >> 1;
+    const uint32_t o = off + (uint32_t)(((((size_t)(m >> 4) * (FF / 32) + (f >> 5)) * 64 + ((f & 31) >> 3) * 16 +
+                                          (m & 15)) * 16) + (f & 7) * 2);
+    st_b32(ws, o, pack_bf16x2(gelu_tanh(v[0]) * v[1], gelu_tanh(v[2]) * v[3]));
   }
 };
 
@@ -109,10 +114,9 @@ struct EpiPart : NoPre {  // fp32 partial sums [split][MP][1024]
 // ---------------------------------------------------------------- norm rows
 // One wave per token row; lane holds columns 4 lane + 256 k + i. MODE 0: x = embed(x_t);
 // MODE 1: x += gate * sum of the K-split partials; MODE 2: as 1, then final norm + action
-// projection + Euler update of x_t. xn is row-major [M][1024] for the 128-token tiles, or with FRAG in
-// MFMA fragment order for the tall tile (column d of token m: 8 bytes of the slot (k-quarter
-// (d % 32) / 8, token m % 16) of fragment (m / 16, d / 32)).
-template <int MODE, bool FRAG = false>
+// projection + Euler update of x_t. xn is stored in MFMA fragment order (column d of token m: 8 bytes
+// of the slot (k-quarter (d % 32) / 8, token m % 16) of fragment (m / 16, d / 32)).
+template <int MODE>
 __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xtr, const float* gate, const float* scale, const float* shift,
                            float dt) {
   const Layout& L = p.L;
@@ -182,10 +186,15 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
       for (int k = 0; k < 4; k++) {
         const int d = 4 * lane + 256 * k;
         st_b128(ws, (uint32_t)(L.x + ((size_t)m * D + d) * 4), as_u32x4(x[k]));
-        const uint32_t xa = FRAG ? (uint32_t)((((size_t)(m >> 4) * (D / 32) + (d >> 5)) * 64 + ((d & 31) >> 3) * 16 +
-                                                (m & 15)) * 16 + (d & 7) * 2)
-                                 : (uint32_t)(((size_t)m * D + d) * 2);
-        st_b64(ws, (uint32_t)L.xn + xa, u32x2{pack_bf16x2(h[k][0], h[k][1]), pack_bf16x2(h[k][2], h[k][3])});
+        // 16-byte fragment slots: lanes (2j, 2j + 1) hold columns 8j .. 8j + 7 of this k; the even
+        // lane stores the slot for even k, the odd lane for odd k
+        const unsigned lo = pack_bf16x2(h[k][0], h[k][1]), hi = pack_bf16x2(h[k][2], h[k][3]);
+        const unsigned plo = swap_adj(lo), phi = swap_adj(hi);
+        if ((lane & 1) == (k & 1)) {
+          const int c = d & ~7;
+          const uint32_t xa = (uint32_t)((((size_t)(m >> 4) * (D / 32) + (c >> 5)) * 64 + ((c & 31) >> 3) * 16 + (m & 15)) * 16);
+          st_b128(ws, (uint32_t)L.xn + xa, (lane & 1) ? u32x4{plo, phi, lo, hi} : u32x4{lo, hi, plo, phi});
+        }
       }
     } else {
       float acc = 0.f;  // lane a < 32 ends with v[a]
@@ -246,10 +255,11 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
   const int NL = p.NL;
   const float dt = -1.0f / (float)p.S;
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  const uint32_t mb16 = (uint32_t)((L.M + 15) / 16 * 16);  // tokens of the fragment-ordered operands
+  GemmArgsF gxf{make_rsrc(p.ws + L.xn, mb16 * D * 2), nullptr, D / 32, D, L.M};
   GemmArgs gx{reinterpret_cast<const bf16*>(p.ws + L.xn), nullptr, D, D, L.M};
   GemmArgs ga{reinterpret_cast<const bf16*>(p.ws + L.attn), nullptr, QD, QD, L.M};
   GemmArgs gh{reinterpret_cast<const bf16*>(p.ws + L.h), nullptr, FF, FF, L.M};
-  GemmArgsF gxf{make_rsrc(p.ws + L.xn, (uint32_t)((L.M + 15) / 16 * 16) * D * 2), nullptr, D / 32, D, L.M};
 #pragma unroll 1
   for (int step = 0; step < p.S; step++) {
 #pragma unroll 1
@@ -267,7 +277,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       {
         EpiQKV e{ws, kc, vc, p.rope_cos, p.rope_sin, (uint32_t)L.qf, L.NQT, p.Tv, NL, p.Lmax, p.Lp, l, 0};
         gx.W = p.w1 + (size_t)l * 2560 * D;
-        gemm_stage<3, 4>(gx, 2560, D, 1, e);  // 96-token tiles: 180 items fill more of the 256 CUs than 140
+        gemm_stage<3, 4, true>(gx, 2560, D, 1, e);  // 96-token tiles: 180 items fill more of the 256 CUs than 140
       }
       mark(p, 1, t0);
       grid_sync(grid);
@@ -283,17 +293,17 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       {
         EpiPart e{{}, ws, (uint32_t)L.part, L.MP, 0};
         ga.W = p.wo + (size_t)l * D * QD;
-        gemm_stage<4, 4>(ga, D, QD, KSPLIT, e);
+        gemm_stage<4, 4, true>(ga, D, QD, KSPLIT, e);
       }
       mark(p, 4, t0);
       grid_sync(grid);
       mark(p, 9, t0);
-      stage_norm<1, true>(p, ws, xtr, mod_in + 2 * D, mod_post, mod_post + D, 0.f);
+      stage_norm<1>(p, ws, xtr, mod_in + 2 * D, mod_post, mod_post + D, 0.f);
       mark(p, 5, t0);
       grid_sync(grid);
       mark(p, 9, t0);
       {
-        EpiGeluT e{ws, (uint32_t)L.h, 0};
+        EpiGeluF e{ws, (uint32_t)L.h, 0};
         gxf.W = p.w2 + (size_t)l * 8192 * D;
         gemm_stage_tall(gxf, 8192, D, 1, e);
       }
@@ -303,7 +313,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       {
         EpiPart e{{}, ws, (uint32_t)L.part, L.MP, 0};
         gh.W = p.w3 + (size_t)l * D * FF;
-        gemm_stage<4, 4>(gh, D, FF, KSPLIT, e);
+        gemm_stage<4, 4, true>(gh, D, FF, KSPLIT, e);
       }
       mark(p, 7, t0);
       grid_sync(grid);

@@ -521,7 +521,7 @@ __device__ __forceinline__ void gemm_stage_tall(const GemmArgsF& g, int N, int K
 // `counters` holds one zeroed word per output tile; `flag_lds` is an LDS word outside the GEMM ring.
 constexpr int FIXUP_MAX_KS = 16;
 
-template <int WM, int WN, class Fin>
+template <int WM, int WN, bool AF = false, class Fin>
 __device__ __forceinline__ void gemm_stage_fixup(const GemmArgs& g, int N, int K, int ksplit, rsrc_t ws,
                                                  uint32_t part_off, int MP, unsigned* counters, uint32_t flag_lds,
                                                  Fin& fin) {
@@ -546,7 +546,7 @@ __device__ __forceinline__ void gemm_stage_fixup(const GemmArgs& g, int N, int K
 #pragma unroll 1
     for (int it = vwg(); it < items; it += NWG) {
       const int mt = it % nm, nt = it / nm;
-      gemm_tile<WM, WN>(g, mt * S::BM, nt * S::BN, 0, K, d);
+      gemm_tile<WM, WN, AF>(g, mt * S::BM, nt * S::BN, 0, K, d);
     }
     return;
   }
@@ -557,7 +557,7 @@ __device__ __forceinline__ void gemm_stage_fixup(const GemmArgs& g, int N, int K
   for (int it = vwg(); it < items; it += NWG) {
     const int mt = it % nm, rest = it / nm, nt = rest % nn, sp = rest / nn;
     epi.split = sp;
-    gemm_tile<WM, WN>(g, mt * S::BM, nt * S::BN, sp * kc, sp * kc + kc, epi);
+    gemm_tile<WM, WN, AF>(g, mt * S::BM, nt * S::BN, sp * kc, sp * kc + kc, epi);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are complete
     __syncthreads();
     if (threadIdx.x == 0) {

@@ -108,6 +108,13 @@ struct Params {
   int NL, Lk, Lkmax, Tv, adim, S, B, xt_rows;
 };
 
+// Byte offset of element (token m, column c) of a [M][K] bf16 activation stored in MFMA fragment order
+// (the GEMMs' token operand): fragment (m / 16, c / 32) of 1 KB, 16-byte slot (k-quarter (c % 32) / 8,
+// token m % 16), element c % 8.
+__device__ __forceinline__ uint32_t afrag(int m, int c, int K) {
+  return (uint32_t)((((size_t)(m >> 4) * (K / 32) + (c >> 5)) * 64 + ((c & 31) >> 3) * 16 + (m & 15)) * 16 + (c & 7) * 2);
+}
+
 struct FinBias {  // y[m][n..n+3] = sum + bias (fp32)
   rsrc_t ws;
   uint32_t off;
@@ -261,8 +268,12 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
       for (int k = 0; k < 3; k++) {
         const int d = 4 * lane + 256 * k;
         st_b128(ws, (uint32_t)(L.x + ((size_t)m * D + d) * 4), as_u32x4(x[k]));
-        st_b64(ws, (uint32_t)(L.xn + ((size_t)m * D + d) * 2),
-               u32x2{pack_bf16x2(h[k][0], h[k][1]), pack_bf16x2(h[k][2], h[k][3])});
+        // xn in fragment order, whole 16-byte slots: lanes (2j, 2j + 1) hold columns 8j .. 8j + 7 of
+        // this k; the even lane stores the slot for even k, the odd lane for odd k
+        const unsigned lo = pack_bf16x2(h[k][0], h[k][1]), hi = pack_bf16x2(h[k][2], h[k][3]);
+        const unsigned plo = swap_adj(lo), phi = swap_adj(hi);
+        if ((lane & 1) == (k & 1))
+          st_b128(ws, (uint32_t)L.xn + afrag(m, d & ~7, D), (lane & 1) ? u32x4{plo, phi, lo, hi} : u32x4{lo, hi, plo, phi});
       }
     } else {
       float acc = 0.f;  // lane a < adim ends with v[a]
@@ -421,7 +432,7 @@ __device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, const YSr
         const int mo = b * p.Tv + t;
 #pragma unroll
         for (int dt = 0; dt < 6; dt++)
-          st_b64(ws, (uint32_t)(L.attn + ((size_t)mo * D + HD * h + 16 * dt + 4 * g4) * 2),
+          st_b64(ws, (uint32_t)L.attn + afrag(mo, HD * h + 16 * dt + 4 * g4, D),
                  u32x2{pack_bf16x2(o[dt][0], o[dt][1]), pack_bf16x2(o[dt][2], o[dt][3])});
       }
     }
@@ -558,7 +569,7 @@ __device__ __forceinline__ void stage_comb(const Params& p, rsrc_t ws) {
     }
     if (valid) {
       const float inv = 1.0f / den;
-      st_b64(ws, (uint32_t)(L.attn + (((size_t)b * p.Tv + t) * D + HD * h + d0) * 2),
+      st_b64(ws, (uint32_t)L.attn + afrag(b * p.Tv + t, HD * h + d0, D),
              u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)});
     }
   }
@@ -607,16 +618,23 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
   // applies the activation), which spreads the reduction over all workgroups.
   constexpr bool FIX = WM == 1;
   unsigned* cnt = reinterpret_cast<unsigned*>(p.ws + L.cnt);
-  auto gemm = [&](GemmArgs& g, const bf16* W, int N, int K, int ks, uint32_t part, uint32_t yfin, const float* bias) {
+  // xn and attn are fragment-ordered (AF); h stays row-major, written whole rows at a time by the
+  // gate/up epilogue (as fragments, 4 bytes per lane into 16-byte slots, GU took 14.2 instead of
+  // 11.3 µs per layer at batch 16)
+  auto gemm = [&](auto af, GemmArgs& g, const bf16* W, int N, int K, int ks, uint32_t part, uint32_t yfin,
+                  const float* bias) {
+    constexpr bool AF = decltype(af)::value;
     g.W = W;
     if constexpr (FIX) {
       FinBias f{ws, yfin, N, bias};
-      gemm_stage_fixup<WM, WN>(g, N, K, ks, ws, part, L.MP, cnt, RING_BYTES, f);
+      gemm_stage_fixup<WM, WN, AF>(g, N, K, ks, ws, part, L.MP, cnt, RING_BYTES, f);
     } else {
       EpiPartN e{{}, ws, part, L.MP, N, 0};
-      gemm_stage<WM, WN>(g, N, K, ks, e);
+      gemm_stage<WM, WN, AF>(g, N, K, ks, e);
     }
   };
+  const std::true_type frag;
+  const std::false_type rows;
 #pragma unroll 1
   for (int step = 0; step < p.S; step++) {
 #pragma unroll 1
@@ -632,40 +650,40 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
       else
         stage_norm<1, FIX>(p, ws, xtr, ydn, mo - 9 * D + 8 * D, mo, mo + D, 0.f);  // gate: mlp of layer l-1
       sync(0);
-      gemm(gx, p.w_qkv + (size_t)l * QKVN * D, QKVN, D, L.ks_qkv, (uint32_t)L.pqkv, (uint32_t)L.yqkv, yqkv.bias);
+      gemm(frag, gx, p.w_qkv + (size_t)l * QKVN * D, QKVN, D, L.ks_qkv, (uint32_t)L.pqkv, (uint32_t)L.yqkv, yqkv.bias);
       sync(1);
       stage_satt<FIX>(p, ws, yqkv);
       sync(2);
-      gemm(ga, p.w_so + (size_t)l * D * D, D, D, L.ks_d, (uint32_t)L.part, (uint32_t)L.yo, yso.bias);
+      gemm(frag, ga, p.w_so + (size_t)l * D * D, D, D, L.ks_d, (uint32_t)L.part, (uint32_t)L.yo, yso.bias);
       sync(3);
       stage_norm<1, FIX>(p, ws, xtr, yso, mo + 2 * D, mo + 3 * D, mo + 4 * D, 0.f);
       sync(4);
-      gemm(gx, p.w_cq + (size_t)l * D * D, D, D, L.ks_d, (uint32_t)L.pq, (uint32_t)L.yq, ycq.bias);
+      gemm(frag, gx, p.w_cq + (size_t)l * D * D, D, D, L.ks_d, (uint32_t)L.pq, (uint32_t)L.yq, ycq.bias);
       sync(5);
       stage_catt<FIX>(p, ws, l, ycq);
       sync(6);
       stage_comb(p, ws);
       sync(7);
-      gemm(ga, p.w_co + (size_t)l * D * D, D, D, L.ks_d, (uint32_t)L.part, (uint32_t)L.yo, yco.bias);
+      gemm(frag, ga, p.w_co + (size_t)l * D * D, D, D, L.ks_d, (uint32_t)L.part, (uint32_t)L.yo, yco.bias);
       sync(8);
       stage_norm<1, FIX>(p, ws, xtr, yco, mo + 5 * D, mo + 6 * D, mo + 7 * D, 0.f);
       sync(9);
       gx.W = p.w_gu + (size_t)l * GUN * D;
       if constexpr (FIX) {
         FinSiluGate f{ws, (uint32_t)L.h, p.b_gu + (size_t)l * GUN};
-        gemm_stage_fixup<WM, WN>(gx, GUN, D, L.ks_gu, ws, (uint32_t)L.pgu, L.MP, cnt, RING_BYTES, f);
+        gemm_stage_fixup<WM, WN, true>(gx, GUN, D, L.ks_gu, ws, (uint32_t)L.pgu, L.MP, cnt, RING_BYTES, f);
       } else if (L.ks_gu == 1) {  // one pass of tiles covers the grid: gate fused into the epilogue
         EpiSiluGate e{{}, ws, (uint32_t)L.h, p.b_gu + (size_t)l * GUN, 0};
-        gemm_stage<WM, WN>(gx, GUN, D, 1, e);
+        gemm_stage<WM, WN, true>(gx, GUN, D, 1, e);
         mark(p, 10, t0);
       } else {
         EpiPartN e{{}, ws, (uint32_t)L.pgu, L.MP, GUN, 0};
-        gemm_stage<WM, WN>(gx, GUN, D, L.ks_gu, e);
+        gemm_stage<WM, WN, true>(gx, GUN, D, L.ks_gu, e);
         sync(10);
         stage_gate(p, ws, l);
       }
       sync(11);
-      gemm(gh, p.w_dn + (size_t)l * D * FF, D, FF, L.ks_dn, (uint32_t)L.part, (uint32_t)L.yo,
+      gemm(rows, gh, p.w_dn + (size_t)l * D * FF, D, FF, L.ks_dn, (uint32_t)L.part, (uint32_t)L.yo,
            p.b_dn + (size_t)l * D);
       sync(12);
     }

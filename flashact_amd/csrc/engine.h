@@ -448,19 +448,20 @@ __device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, 
         for (int i = 0; i < WM; i++) acc[j][i] = mfma16(wfr[j], a[WM * ks + i], acc[j][i]);
         if (ks + 1 < 4) wfr[j] = rd(ks + 1, j);
       }
-      if (s + 1 < ns)
+      // Unconditional (the last step's loads read past k1: another split's fragments, or zeros
+      // past the descriptor's bound, never used). Behind a branch, the compiler's wait analysis
+      // (which does not pair the branches of one condition) waited for every outstanding load,
+      // the weight copy just issued included, before the first MFMAs of each step.
 #pragma unroll
-        for (int i = 0; i < WM; i++) load_a(s + 1, WM * ks + i);
+      for (int i = 0; i < WM; i++) load_a(s + 1, WM * ks + i);
       __builtin_amdgcn_sched_barrier(0);
     }
     // Everything but this step's loads has landed: stage (s + 1) % 4 (copied two steps ago) for this
     // wave; the barrier makes it every wave's and frees stage s % 4.
     if (s + 3 < ns)
       vm_wait<8 + NA>();
-    else if (s + 1 < ns)
-      vm_wait<NA>();
     else
-      vm_wait<0>();
+      vm_wait<NA>();
     __syncthreads();
   }
   if (16 * tb0 >= g.M) return;

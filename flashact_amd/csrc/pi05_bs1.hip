@@ -793,16 +793,19 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
   const uint32_t vl = (uint32_t)l * HD * p.Lmax * 2;  // layer base, vtcache [256][Lmax]
   const uint32_t vstep = 16 * p.Lmax * 2;             // 16 dims
   if (kbeg >= kend) issue_suffix();
-#pragma unroll 1
-  for (int kb = kbeg; kb < kend; kb += 32) {
-    const bool first = kb == kbeg;
+  // One 32-key block; the first comes from the ring pages, later ones from the caches. The first is
+  // peeled (`first` a compile-time constant): as an if / else inside the loop, the two arms became two
+  // conditional blocks in sequence, and the compiler's waits in the page arm covered the loads of
+  // the cache arm, i.e. waited out this step's suffix keys before the P V MFMAs they should overlap.
+  auto block = [&](int kb, auto first_c) __attribute__((always_inline)) {
+    constexpr bool first = decltype(first_c)::value;
     const int kg0 = kb + c.lq * 4;
     f32x4 s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
       u32x4 kf[8];
       const int key = kb + kt * 16 + c.lr;
-      if (first) {  // the ring page
+      if constexpr (first) {  // the ring page
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
           kf[ks] = *reinterpret_cast<const u32x4*>(fa_lds + kslot + (kt * 8 + ks) * 1024 + c.lane * 16);
@@ -865,7 +868,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
 #pragma unroll
       for (int h2 = 0; h2 < 2; h2++) {
         const int kg = kg0 + 16 * h2;
-        if (first) {  // the ring page
+        if constexpr (first) {  // the ring page
           const int o8 = 16 * h2 + 4 * c.lq;  // key offset within the 32-key block
           const uint32_t ad = vslot + (c.lr + 16 * (o8 >> 3)) * 16 + (o8 & 7) * 2 + half * 8 * 1024;
 #pragma unroll
@@ -885,6 +888,11 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
         o[dt] = mfma16(va, pb, o[dt] * alpha);
       }
     }
+  };
+  if (kbeg < kend) {
+    block(kbeg, std::true_type{});
+#pragma unroll 1
+    for (int kb = kbeg + 32; kb < kend; kb += 32) block(kb, std::false_type{});
   }
   if (nsfx > 0) {
     // This step's keys: one 16-key S^T tile whose rows 0 (token r) and 1 (token r + 32) are valid;

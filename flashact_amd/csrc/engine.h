@@ -213,6 +213,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
 #pragma unroll
     for (int i = 0; i < WM; i++) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   __builtin_amdgcn_s_waitcnt(0);  // earlier stores / loads of this wave are complete
+  // Epilogue inputs (e.g. RoPE factors) are requested before the first copies, so their latency
+  // passes under the prologue wait instead of after the last MFMA.
+  typename Epi::Pre pre[WN][WM];
+  if constexpr (Epi::kRowBytes == 0) {
+#pragma unroll
+    for (int j = 0; j < WN; j++)
+#pragma unroll
+      for (int i = 0; i < WM; i++) {
+        const int m = m0 + 16 * (wm * WM + i) + lr;
+        pre[j][i] = epi.pre(n0 + 16 * (wn * WN + j) + 4 * lq, m < g.M ? m : 0);
+      }
+  }
   issue(0);
 #pragma unroll 1
   for (int s = 0; s < ns; s++) {
@@ -296,16 +308,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
         }
       }
   } else {
-    // Epilogue inputs (e.g. RoPE factors) are fetched for every block before the first store, so
-    // the loads are not serialised behind stores the compiler must assume may alias them.
-    typename Epi::Pre pre[WN][WM];
-#pragma unroll
-    for (int j = 0; j < WN; j++)
-#pragma unroll
-      for (int i = 0; i < WM; i++) {
-        const int m = m0 + 16 * (wm * WM + i) + lr;
-        pre[j][i] = epi.pre(n0 + 16 * (wn * WN + j) + 4 * lq, m < g.M ? m : 0);
-      }
 #pragma unroll
     for (int j = 0; j < WN; j++)
 #pragma unroll

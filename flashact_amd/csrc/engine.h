@@ -132,6 +132,21 @@ __device__ __forceinline__ void grid_sync(Grid& g) {
 }
 
 // ---------------------------------------------------------------- tiled GEMM
+// A row-out epilogue's pack(n, v) or, when it takes its fetched inputs, pack(n, v, pre).
+template <class E>
+__device__ __forceinline__ auto pack_pre(const E& e, int n, f32x4 v, const typename E::Pre& p, int)
+    -> decltype(e.pack(n, v, p)) {
+  return e.pack(n, v, p);
+}
+template <class E>
+__device__ __forceinline__ u32x4 pack_pre(const E& e, int n, f32x4 v, const typename E::Pre&, long) {
+  return e.pack(n, v);
+}
+template <class E>
+__device__ __forceinline__ u32x4 pack_pre(const E& e, int n, f32x4 v, const typename E::Pre& p) {
+  return pack_pre(e, n, v, p, 0);
+}
+
 // C^T[n][m] = sum_k W[n][k] A[m][k] over k in [k0, k1) for a BM x BN tile (BM = 32 WM, BN = 32 WN).
 // Waves form a 2 x 2 grid; wave (wm, wn) computes WM x WN MFMA blocks of 16 x 16 with
 // v_mfma_f32_16x16x32_bf16 (A operand = 16 weight rows, B operand = 16 tokens), so after the loop
@@ -216,7 +231,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
   // Epilogue inputs (e.g. RoPE factors) are requested before the first copies, so their latency
   // passes under the prologue wait instead of after the last MFMA.
   typename Epi::Pre pre[WN][WM];
-  if constexpr (Epi::kRowBytes == 0) {
+  {
 #pragma unroll
     for (int j = 0; j < WN; j++)
 #pragma unroll
@@ -274,7 +289,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
 #pragma unroll
       for (int i = 0; i < WM; i++) {
         const int ml = 16 * (wm * WM + i) + lr, nl = 16 * (wn * WN + j) + 4 * lq;
-        const u32x4 v = epi.pack(n0 + nl, acc[j][i]);
+        const u32x4 v = pack_pre(epi, n0 + nl, acc[j][i], pre[j][i]);
         const uint32_t a = (uint32_t)(ml * RP + (nl >> 2) * OB);
         if constexpr (OB == 16)
           *reinterpret_cast<u32x4*>(lds + a) = v;
@@ -299,7 +314,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
       for (int i = 0; i < WM; i++) {
         const int ml = 16 * (wm * WM + i) + lr, nl = 16 * (wn * WN + j) + 4 * lq;
         if (m0 + ml < g.M) {
-          const u32x4 v = epi.pack(n0 + nl, acc[j][i]);
+          const u32x4 v = pack_pre(epi, n0 + nl, acc[j][i], pre[j][i]);
           const uint32_t o = epi.row_off(m0 + ml, n0) + (uint32_t)((nl >> 2) * OB);
           if constexpr (OB == 16)
             st_b128(epi.ws, o, v);
@@ -365,9 +380,9 @@ __device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int 
 //   sub-steps 0-1, and after each sub-step the next step's WM activation fragments of that sub-step,
 //   into the registers its MFMAs have just read (one activation register set: 16 WM VGPRs, which keeps
 //   the persistent kernels free of spills; two sets spilled 32-60 VGPRs in the prefill).
-// Measured in isolation on L2-resident operands (`_work` probe, 256 CUs): the tall tile 7.5 µs per
-// 128 x 128 x 1024 of work against 10.2-10.6 µs for gemm_tile; in the prefill kernel, gate/up
-// 181 -> 133 µs and down 86 -> 73 µs per layer.
+// Measured in isolation on L2-resident operands (a standalone probe, 256 CUs): the tall tile 7.5 µs
+// per 128 x 128 x 1024 of work against 10.2-10.6 µs for gemm_tile; in the prefill kernel, gate/up
+// 181 -> 114 µs and down 86 -> 62 µs per layer (128 x 128 tiles -> this tile).
 struct GemmArgsF {
   rsrc_t A;        // fragment-ordered activations, bounded to ceil(M / 16) token blocks (loads past: 0)
   const bf16* W;   // [N][ldw] weights

@@ -140,15 +140,16 @@ struct FinSiluGate {  // columns 2f, 2f+1 = gate f, up f -> h[m][f] = silu(g + b
 // straight from the tile (bf16, whole 128-byte rows through LDS), instead of fp32 partials, a
 // separate gate stage and its grid barrier: batch 16 43.4 -> 40.9 ms per launch (stored in place,
 // 4 bytes into each of 16 rows per instruction, the fused stage took 18.5 instead of 13.2 µs).
-struct EpiSiluGate : NoPre {
+struct EpiSiluGate {
   static constexpr int kRowBytes = 4;
   static constexpr bool kStaged = true;
   rsrc_t ws;
   uint32_t off;
   const float* bias;
   int split;
-  __device__ u32x4 pack(int n, f32x4 v) const {
-    const f32x4 b = *reinterpret_cast<const f32x4*>(bias + n);
+  typedef f32x4 Pre;  // biases of features n..n+3, fetched before the tile's first copies
+  __device__ Pre pre(int n, int) const { return *reinterpret_cast<const f32x4*>(bias + n); }
+  __device__ u32x4 pack(int, f32x4 v, f32x4 b) const {
     return u32x4{pack_bf16x2(silu(v[0] + b[0]) * (v[1] + b[1]), silu(v[2] + b[2]) * (v[3] + b[3])), 0u, 0u, 0u};
   }
   __device__ uint32_t row_off(int m, int n0) const { return off + (uint32_t)(((size_t)m * FF + (n0 >> 1)) * 2); }
@@ -673,7 +674,7 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
         FinSiluGate f{ws, (uint32_t)L.h, p.b_gu + (size_t)l * GUN};
         gemm_stage_fixup<WM, WN, true>(gx, GUN, D, L.ks_gu, ws, (uint32_t)L.pgu, L.MP, cnt, RING_BYTES, f);
       } else if (L.ks_gu == 1) {  // one pass of tiles covers the grid: gate fused into the epilogue
-        EpiSiluGate e{{}, ws, (uint32_t)L.h, p.b_gu + (size_t)l * GUN, 0};
+        EpiSiluGate e{ws, (uint32_t)L.h, p.b_gu + (size_t)l * GUN, 0};
         gemm_stage<WM, WN, true>(gx, GUN, D, 1, e);
         mark(p, 10, t0);
       } else {

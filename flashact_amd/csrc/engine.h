@@ -16,15 +16,43 @@
 namespace fa {
 namespace eng {
 
-constexpr int NWG = 256;   // workgroups (one per CU)
-constexpr int NTHR = 256;  // threads per workgroup (4 waves)
+// Waves per workgroup: 4 (one per SIMD, up to 512 VGPR + AGPR per lane) unless the kernel's source
+// sets FA_ENG_NWAVE to 8 before including this header (two waves per SIMD, at most 256 registers per
+// lane in every stage; a single wave keeps the MFMA pipe about 60 % busy, two about 85 %).
+#ifndef FA_ENG_NWAVE
+#define FA_ENG_NWAVE 4
+#endif
+constexpr int NWG = 256;                // workgroups (one per CU)
+constexpr int NWAVE = FA_ENG_NWAVE;     // waves per workgroup
+constexpr int NTHR = 64 * NWAVE;        // threads per workgroup
+static_assert(NWAVE == 4 || NWAVE == 8, "4 or 8 waves per workgroup");
 
 extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
 
-__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
-__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// With 8 waves (256 registers per lane) the indices pass through an empty asm, so the compiler
+// derives each stage's addresses inside the stage instead of hoisting them out of the layer loop and
+// keeping them live across every other stage (8-wave prefill: 171 -> 20 spilled VGPRs). With 4 waves
+// the registers are there, and recomputing the addresses per stage measured slower (batch 16 19.09 ->
+// 19.42 ms).
+__device__ __forceinline__ int wave_id() {
+  int w = threadIdx.x >> 6;
+  if (NWAVE == 8) asm volatile("" : "+v"(w));
+  return __builtin_amdgcn_readfirstlane(w);
+}
+__device__ __forceinline__ int lane_id() {
+  int l = threadIdx.x & 63;
+  if (NWAVE == 8) asm volatile("" : "+v"(l));
+  return l;
+}
 // XCD-major virtual workgroup index: workgroup b runs on XCD b % 8; v = xcd * 32 + rank.
-__device__ __forceinline__ int vwg() { return (blockIdx.x & 7) * 32 + (blockIdx.x >> 3); }
+__device__ __forceinline__ int vwg() {
+  int v = (blockIdx.x & 7) * 32 + (blockIdx.x >> 3);
+  if (NWAVE == 8) {
+    asm volatile("" : "+v"(v));
+    v = __builtin_amdgcn_readfirstlane(v);
+  }
+  return v;
+}
 
 // ---------------------------------------------------------------- global <-> LDS copies
 // global_load_lds_dwordx4: lane i copies 16 bytes from its address to LDS m0 + 16 i, so one
@@ -175,7 +203,7 @@ struct GemmShape {
   static constexpr int BM = 32 * WM, BN = 32 * WN;
   static constexpr int GA = (BM + 63) / 64, GW = (BN + 63) / 64;  // 64-row groups
   static constexpr int NI = 16 * (GA + GW);                       // copy instructions per step
-  static constexpr int IPW = NI / 4;                              // per wave
+  static constexpr int IPW = NI / NWAVE;                          // per wave
   static constexpr uint32_t PITCH = 1040;
   static constexpr uint32_t STEP = (uint32_t)NI * PITCH;
   static constexpr uint32_t LDS = 2 * STEP;
@@ -186,12 +214,14 @@ template <int WM, int WN, bool AF = false, class Epi>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int k0, int k1, Epi& epi) {
   using S = GemmShape<WM, WN>;
   const int w = wave_id(), lane = lane_id(), lr = lane & 15, lq = lane >> 4;
-  const int wm = w & 1, wn = w >> 1;
-  // this wave's copy instructions of every step: f = w + 4 j; lane -> (row slot lq, 16-byte chunk lr)
+  const int wm = w & 1, wn = (w >> 1) & 1;
+  // Waves 0-3 compute (2 x 2); with 8 waves, waves 4-7 share the copies and barriers only.
+  const bool cw = NWAVE == 4 || w < 4;
+  // this wave's copy instructions of every step: f = w + NWAVE j; lane -> (row slot lq, 16-byte chunk lr)
   const unsigned char* src[S::IPW];
 #pragma unroll
   for (int j = 0; j < S::IPW; j++) {
-    const int f = w + 4 * j;
+    const int f = w + NWAVE * j;
     if (f < 16 * S::GA) {
       if constexpr (AF) {
         // blocks past the tile or past M copy the last token block of the operand (results discarded)
@@ -215,7 +245,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
     const uint32_t base = (uint32_t)(s & 1) * S::STEP;
 #pragma unroll
     for (int j = 0; j < S::IPW; j++) {
-      const int f = w + 4 * j;
+      const int f = w + NWAVE * j;
       if (f < 16 * S::GA)
         dma16<true>(src[j] + (AF ? 4096 : 256) * s, lds_addr(base + f * S::PITCH));
       else
@@ -231,7 +261,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
   // Epilogue inputs (e.g. RoPE factors) are requested before the first copies, so their latency
   // passes under the prologue wait instead of after the last MFMA.
   typename Epi::Pre pre[WN][WM];
-  {
+  if (cw) {
 #pragma unroll
     for (int j = 0; j < WN; j++)
 #pragma unroll
@@ -246,6 +276,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
     vm_wait<0>();
     __syncthreads();  // step s landed for every wave; every wave is done with step s - 1
     if (s + 1 < ns) issue(s + 1);
+    if (!cw) continue;
     const uint32_t base = (uint32_t)(s & 1) * S::STEP;
     // fragments of k sub-step ks + 1 are read while the MFMAs of ks run (double-buffered)
     u32x4 a[2][WM], b[2][WN];
@@ -287,7 +318,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
 #pragma unroll
     for (int j = 0; j < WN; j++)
 #pragma unroll
-      for (int i = 0; i < WM; i++) {
+      for (int i = 0; i < WM && cw; i++) {
         const int ml = 16 * (wm * WM + i) + lr, nl = 16 * (wn * WN + j) + 4 * lq;
         const u32x4 v = pack_pre(epi, n0 + nl, acc[j][i], pre[j][i]);
         const uint32_t a = (uint32_t)(ml * RP + (nl >> 2) * OB);
@@ -313,7 +344,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
 #pragma unroll
       for (int i = 0; i < WM; i++) {
         const int ml = 16 * (wm * WM + i) + lr, nl = 16 * (wn * WN + j) + 4 * lq;
-        if (m0 + ml < g.M) {
+        if (cw && m0 + ml < g.M) {
           const u32x4 v = pack_pre(epi, n0 + nl, acc[j][i], pre[j][i]);
           const uint32_t o = epi.row_off(m0 + ml, n0) + (uint32_t)((nl >> 2) * OB);
           if constexpr (OB == 16)
@@ -328,7 +359,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
 #pragma unroll
       for (int i = 0; i < WM; i++) {
         const int m = m0 + 16 * (wm * WM + i) + lr;
-        if (m < g.M) epi(n0 + 16 * (wn * WN + j) + 4 * lq, m, acc[j][i], pre[j][i]);
+        if (cw && m < g.M) epi(n0 + 16 * (wn * WN + j) + 4 * lq, m, acc[j][i], pre[j][i]);
       }
   }
 }
@@ -363,12 +394,12 @@ __device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int 
 }
 
 // ---------------------------------------------------------------- direct-operand GEMM tiles
-// gemm_tile_d<TW, WM>: a (16 WM TW)-token x 128-feature tile whose token operand skips LDS. The 4 waves
-// form TW rows along the tokens and 4 / TW columns along the features; wave (wt, wf) computes WM token
-// blocks x WN = 2 TW feature blocks of 16 x 16. The tall tile (TW = 4, WM = 4: 256 x 128, a wave
-// holds 64 tokens x 128 features, 32 MFMAs per 32-k sub-step for 12 fragment reads, against 16 for 8
-// in gemm_tile) is for GEMMs with many output tiles; the square one (TW = 2: 128 or 96 x 128, the
-// shape of gemm_tile) for the rest.
+// gemm_tile_d<TW, WM>: a (16 WM TW)-token x 128-feature tile whose token operand skips LDS. The NWAVE
+// waves form TW rows along the tokens and NWAVE / TW columns along the features; wave (wt, wf) computes
+// WM token blocks x WN feature blocks of 16 x 16. The tall tile (TW = NWAVE, WM = 4: 256 x 128 with 4
+// waves, 512 x 128 with 8; a wave holds 64 tokens x 128 features, 32 MFMAs per 32-k sub-step for 12
+// fragment reads, against 16 for 8 in gemm_tile) is for GEMMs with many output tiles; the square one
+// (4 waves, TW = 2: 128 or 96 x 128, the shape of gemm_tile) for the rest.
 // * Activations are stored in MFMA fragment order (fragment (token block tb, k-step kk) = 1 KB at
 //   (tb KF + kk) * 1024, lane l = lr + 16 q holding token lr, k 8q..8q+7 at 16 l) and loaded straight
 //   into registers, a whole 128-k step ahead of their use (the waves of one token row load the same
@@ -400,11 +431,14 @@ struct HasPre<E, std::void_t<typename E::Pre>> : std::true_type {};
 // (gemm_tile's interface) gets epi(n, m, v, pre) with every block's pre fetched before the first call.
 template <int TW, int WM, class Epi>
 __device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, int k0, int k1, Epi& epi) {
-  static_assert(TW == 4 || TW == 2, "4 or 2 waves along the tokens");
-  constexpr int FW = 4 / TW, WN = 8 / FW, NA = 4 * WM;
+  static_assert(NWAVE % TW == 0 && (NWAVE / TW == 1 || NWAVE / TW == 2), "TW waves along the tokens");
+  // FW waves along the features; CPW weight copies per wave and step, CPK of them in each of the
+  // step's first two sub-steps (one every JM feature blocks)
+  constexpr int FW = NWAVE / TW, WN = 8 / FW, NA = 4 * WM, CPW = 32 / NWAVE, CPK = CPW / 2, JM = WN / CPK;
+  static_assert(JM >= 1 && WN % CPK == 0, "copy schedule");
   const int w = wave_id(), lane = lane_id(), lr = lane & 15, lq = lane >> 4;
   const int wt = w / FW, wf = w % FW;
-  // copy f = w + 4 j of a step: rows 64 (f / 16) + 16 lq + f % 16 of the tile, 16 B per lane
+  // copy f = w + NWAVE j of a step: rows 64 (f / 16) + 16 lq + f % 16 of the tile, 16 B per lane
   // (readfirstlane returns int: each half is cast to uint32_t before widening, or a low word with
   // bit 31 set would sign-extend over the high word)
   const uint64_t wb = reinterpret_cast<uint64_t>(g.W + (size_t)n0 * g.ldw);
@@ -422,7 +456,7 @@ __device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, 
     for (int i = 0; i < WM; i++) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   u32x4 a[NA];  // [WM ks + i]: token block tb0 + i, k-step ks of the current 128-k step
   auto issue_w = [&](int s, int j) {
-    const int f = w + 4 * j;
+    const int f = w + NWAVE * j;
     dma16s(wbase, wlane + (uint32_t)((64 * (f >> 4) + (f & 15)) * g.ldw * 2 + 256 * s),
            lds_addr((uint32_t)(s & 3) * TALL_ST + f * 1040));
   };
@@ -436,7 +470,7 @@ __device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, 
   for (int s = 0; s < 3; s++)
     if (s < ns)
 #pragma unroll
-      for (int j = 0; j < 8; j++) issue_w(s, j);
+      for (int j = 0; j < CPW; j++) issue_w(s, j);
 #pragma unroll
   for (int q = 0; q < NA; q++) load_a(0, q);
   vm_wait<0>();
@@ -460,7 +494,7 @@ __device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, 
     for (int ks = 0; ks < 4; ks++) {
 #pragma unroll
       for (int j = 0; j < WN; j++) {
-        if (ks < 2 && j % (WN / 4) == 0 && s + 3 < ns) issue_w(s + 3, 4 * ks + j / (WN / 4));
+        if (ks < 2 && j % JM == 0 && s + 3 < ns) issue_w(s + 3, CPK * ks + j / JM);
 #pragma unroll
         for (int i = 0; i < WM; i++) acc[j][i] = mfma16(wfr[j], a[WM * ks + i], acc[j][i]);
         if (ks + 1 < 4) wfr[j] = rd(ks + 1, j);
@@ -476,7 +510,7 @@ __device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, 
     // Everything but this step's loads has landed: stage (s + 1) % 4 (copied two steps ago) for this
     // wave; the barrier makes it every wave's and frees stage s % 4.
     if (s + 3 < ns)
-      vm_wait<8 + NA>();
+      vm_wait<CPW + NA>();
     else
       vm_wait<NA>();
     __syncthreads();
@@ -526,7 +560,7 @@ __device__ __forceinline__ void gemm_stage_d(const GemmArgsF& g, int N, int K, i
 
 template <class Epi>
 __device__ __forceinline__ void gemm_stage_tall(const GemmArgsF& g, int N, int K, int ksplit, Epi& epi) {
-  gemm_stage_d<4, 4>(g, N, K, ksplit, epi);
+  gemm_stage_d<NWAVE, 4>(g, N, K, ksplit, epi);
 }
 
 // Split-K GEMM whose K-splits are summed inside the stage (for small tiles: one workgroup reads the

@@ -72,8 +72,8 @@ struct EpiQKV {
 };
 
 // ---------------------------------------------------------------- attention partials
-// Item (b, kc, qg): keys [128 kc, 128 kc + 128) of sample b against query tiles 16 qg + w + 4 j
-// (wave w, j < 4, two tiles per pass). The chunk's K rows and V^T columns are copied to LDS once,
+// Item (b, kc, qg): keys [128 kc, 128 kc + 128) of sample b against query tiles 16 qg + w + NWAVE j
+// (wave w, j < 16 / NWAVE, two tiles per pass). The chunk's K rows and V^T columns are copied to LDS once,
 // by copies of 4 rows x 256 B (one instruction each, the fast global -> LDS pattern) into blocks
 // at a pitch of 1040 B, so the 16 rows of an MFMA fragment sit in 16 different blocks and a
 // fragment read spreads over all banks:
@@ -113,11 +113,11 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
     // q of a pass's two query tiles (qt, qt + 4); a missing second tile repeats the first
     u32x4 qf[2][8];
     auto load_q = [&](int jp) {
-      const int q0 = QTG * qg + w + 8 * jp;
+      const int q0 = QTG * qg + w + 2 * NWAVE * jp;
       if (q0 >= L.NQT) return;
 #pragma unroll
       for (int q = 0; q < 2; q++) {
-        const int tq = (q == 1 && q0 + 4 >= L.NQT) ? q0 : q0 + 4 * q;
+        const int tq = (q == 1 && q0 + NWAVE >= L.NQT) ? q0 : q0 + NWAVE * q;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
           qf[q][ks] = ldb128<kCpSc1>(ws, (uint32_t)(L.qf + ((((size_t)b * L.NQT + tq) * 8 + ks) * 64 + lane) * 16));
@@ -129,8 +129,8 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
     // count only its own loads, not these copies, so a copy issued after q would be waited for
     // at q's first use.
 #pragma unroll
-    for (int j = 0; j < 16; j++) {  // K block (h, s), f = w + 4 j
-      const int f = w + 4 * j, h = f >> 5, sl = f & 31, kt = sl >> 4, i = sl & 15;
+    for (int j = 0; j < 64 / NWAVE; j++) {  // K block (h, s), f = w + NWAVE j
+      const int f = w + NWAVE * j, h = f >> 5, sl = f & 31, kt = sl >> 4, i = sl & 15;
       int key = key0 + 32 * lq + 8 * (i >> 2) + 4 * kt + (i & 3);
       if (key >= Ltot) key = 0;
       dma16<true>(kb_ + (size_t)key * HD + 128 * h + 8 * lr, lds_addr(f * ATT_PITCH));
@@ -139,16 +139,17 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
     vm_wait<0>();
     __syncthreads();  // K of every wave has landed
 #pragma unroll
-    for (int j = 0; j < 16; j++) {  // V^T block y
-      const int y = w + 4 * j;
+    for (int j = 0; j < 64 / NWAVE; j++) {  // V^T block y
+      const int y = w + NWAVE * j;
       int kg = key0 + 8 * lr;
       if (kg >= Ltot) kg = 0;
       dma16<true>(vb_ + (size_t)(y + 64 * lq) * p.Lmax + kg, lds_addr(ATT_VB + y * ATT_PITCH));
     }
-    // two query tiles per pass (qt, qt + 4): every K / V^T fragment read from LDS feeds 2 MFMAs
+    // two query tiles per pass (qt, qt + NWAVE): every K / V^T fragment read from LDS feeds 2 MFMAs
+    constexpr int NPASS = QTG / (2 * NWAVE);
 #pragma unroll
-    for (int jp = 0; jp < QTG / 8; jp++) {
-      const int qt[2] = {QTG * qg + w + 8 * jp, QTG * qg + w + 8 * jp + 4};
+    for (int jp = 0; jp < NPASS; jp++) {
+      const int qt[2] = {QTG * qg + w + 2 * NWAVE * jp, QTG * qg + w + 2 * NWAVE * jp + NWAVE};
       const bool act = qt[0] < L.NQT;
       if (jp > 0 && !act) break;  // (pass 0 runs its V^T barrier in any case)
       const bool has1 = qt[1] < L.NQT;
@@ -218,18 +219,20 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
         if (!full && ((kend - key0) & 7)) {
           // Keys [kend, ...) of the 8-key group that straddles kend come from cache rows past
           // Ltot: zero them in V^T so that P = 0 meets a finite value. (Groups wholly past Ltot
-          // were copied from key 0 instead.)
-          const int d = threadIdx.x, gk = (kend - key0) >> 3, nv = (kend - key0) & 7;
-          const uint32_t off = ATT_VB + (d & 63) * ATT_PITCH + (d >> 6) * 256 + gk * 16;
-          u32x4 v = lds128(off);
+          // were copied from key 0 instead.) One thread per dim: the first 256 threads.
+          if (threadIdx.x < HD) {
+            const int d = threadIdx.x, gk = (kend - key0) >> 3, nv = (kend - key0) & 7;
+            const uint32_t off = ATT_VB + (d & 63) * ATT_PITCH + (d >> 6) * 256 + gk * 16;
+            u32x4 v = lds128(off);
 #pragma unroll
-          for (int e = 0; e < 4; e++) v[e] &= nv >= 2 * e + 2 ? 0xffffffffu : (nv == 2 * e + 1 ? 0xffffu : 0u);
-          *reinterpret_cast<u32x4*>(lds + off) = v;
+            for (int e = 0; e < 4; e++) v[e] &= nv >= 2 * e + 2 ? 0xffffffffu : (nv == 2 * e + 1 ? 0xffffu : 0u);
+            *reinterpret_cast<u32x4*>(lds + off) = v;
+          }
           __syncthreads();
         }
       }
       if (!act) continue;
-      if (jp + 1 < QTG / 8) load_q(jp + 1);  // the next pass's q, in flight with this pass's P V
+      if (jp + 1 < NPASS) load_q(jp + 1);  // the next pass's q, in flight with this pass's P V
       // O^T = V^T P^T, one 16-dim tile at a time: lane holds O^T[dim 16 dt + 4 lq + i][query row
       // 16 qt + lr]. A pair of dim tiles leaves as one 1 KB block of the partial (attp_off).
       bool st[2], rv[2];
@@ -290,8 +293,10 @@ __device__ __forceinline__ void stage_comb(const P& p, rsrc_t ws) {
   const int dp = l16 >> 1, jh = l16 & 1;  // lane: dims 32 dp + 8 jh .. + 7 and 32 dp + 16 + 8 jh .. + 7
   const int Ltot = p.Lp + p.Tv, nkc = (Ltot + KCH - 1) / KCH;
   const int rows = p.B * NH * p.Tv;
+  // with 8 waves, wave-major (consecutive rows on different CUs first), so rows spread over every CU
+  const int slot = NWAVE == 8 ? wave_id() * NWG + vwg() : vwg() * NWAVE + wave_id();
 #pragma unroll 1
-  for (int R0 = (vwg() * 4 + wave_id()) * 4; R0 < rows; R0 += NWG * 16) {
+  for (int R0 = slot * 4; R0 < rows; R0 += NWG * NWAVE * 4) {
     const int R = R0 + sub;
     const bool valid = R < rows;
     const int Rc = valid ? R : R0;

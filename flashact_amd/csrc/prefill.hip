@@ -1,6 +1,6 @@
 // pi0.5 prefix prefill: the Gemma-2B-shaped backbone (D = 2048, 8 query heads /
 // 1 K/V head of 256, F = 16384) over the Lp prefix tokens of each sample, in ONE cooperative launch
-// of 256 workgroups x 4 waves on the stage engine (engine.h). Its product is the K/V cache the
+// of 256 workgroups x 8 waves on the stage engine (engine.h). Its product is the K/V cache the
 // denoise loop reads: the QKV epilogue writes the RoPE'd keys into kcache rows [0, Lp) and the
 // values into vtcache columns [0, Lp) of every layer, the layout the reference builds with
 // compact_kv and the cache fill after its prefill (src/pi05/pack_weights.py:60-70;
@@ -15,10 +15,13 @@
 //   O    [M x 2048] = attn Wo^T, K split 2 ways -> fp32 partials
 // O, GU and DN read their token operand (attn, xn after N2, h) in MFMA fragment order.
 //   N2   x += sum(partials); xn = rms(x) (1 + w_post), written in MFMA fragment order
-//   GU   [M x 32768] = xn Wgu^T (gate/up rows interleaved, 256 x 128 tiles) -> h = gelu_tanh(g) u
+//   GU   [M x 32768] = xn Wgu^T (gate/up rows interleaved, 512 x 128 tiles) -> h = gelu_tanh(g) u
 //        [M x 16384], fragment order
-//   DN   [M x 2048] = h Wdn^T (256 x 128 tiles), K split 4 ways -> fp32 partials
+//   DN   [M x 2048] = h Wdn^T (512 x 128 tiles), K split 8 ways -> fp32 partials
 // The last layer stops after QKV: its attention and MLP outputs reach no cache entry.
+// Two waves per SIMD (8 per workgroup): the tall MLP tiles keep the MFMA pipe busy about 1.4x as long
+// as one wave per SIMD can, at a budget of 256 registers per lane in every stage.
+#define FA_ENG_NWAVE 8
 #include "engine.h"
 #include "mqa256.h"
 #include "../../include/flashact_mi355x.h"
@@ -31,7 +34,7 @@ using namespace fa::mqa;
 
 constexpr int D = 2048, FF = 16384;
 constexpr int QKVN = QD + 2 * HD;  // 2560 projection rows
-constexpr int KS_O = 2, KS_DN = 4;  // K splits of the O and down projections
+constexpr int KS_O = 2, KS_DN = 8;  // K splits of the O and down projections
 constexpr int MAX_TOKENS = 16384;  // batch x Lp
 
 struct Layout {
@@ -120,53 +123,67 @@ struct EpiPart : NoPre {  // fp32 partial sums [split][MP][2048]
   __device__ uint32_t row_off(int m, int n0) const { return off + (uint32_t)((((size_t)split * MP + m) * D + n0) * 4); }
 };
 
-// One wave per token row; lane holds columns 4 lane + 256 k + i (k < 8). FIRST: x = the prefix
-// hidden states; otherwise x += the sum of the NS K-split partials. Then xn = rms(x) (1 + w), with FRAG
-// in MFMA fragment order (columns c..c+7 of token m, c % 8 = 0: the 16-byte slot (k-quarter
-// (c % 32) / 8, token m % 16) of fragment (m / 16, c / 32)), else row-major [M][2048]. The QKV GEMM
-// after N1 reads the row-major form: fragment slots written 16 bytes at a time by the waves of 16
-// different tokens took N1 from 10.0 to 12.8 µs per layer here (four down partials to sum as well),
-// more than the fragment-order copies save in the GEMM.
+// A token row per wave pair (q, q + 4) of a workgroup (q < 4): half hh = wave / 4 of the pair takes
+// columns [1024 hh, 1024 hh + 1024), the lane columns 4 lane + 256 k + 1024 hh + i (k < 4), and the
+// halves' sums of squares meet in LDS. (One row per wave left half the waves idle at Lp = 968 and
+// needed two rounds of loads for eight down partials: N1 16.2 µs per layer.) Rows go pair-major,
+// row m on workgroup m % 256, so they spread over every CU; every wave runs the same number of rounds,
+// since the exchange is a workgroup barrier. FIRST: x = the prefix hidden states; otherwise x += the
+// sum of the NS K-split partials (in split order). Then xn = rms(x) (1 + w), with FRAG in MFMA fragment
+// order (columns c..c+7 of token m, c % 8 = 0: the 16-byte slot (k-quarter (c % 32) / 8, token m % 16)
+// of fragment (m / 16, c / 32)), else row-major [M][2048]. The QKV GEMM after N1 reads the row-major
+// form: fragment slots written 16 bytes at a time by the waves of 16 different tokens took N1 from
+// 10.0 to 12.8 µs per layer here, more than the fragment-order copies save in the GEMM.
 template <bool FIRST, int NS, bool FRAG>
 __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xin, const float* w) {
+  static_assert(NWAVE == 8, "a row per wave pair");
   const Layout& L = p.L;
-  const int lane = lane_id();
+  const int lane = lane_id(), wv = wave_id(), q = wv & 3, hh = wv >> 2;
+  float* red = reinterpret_cast<float*>(lds);  // [iteration parity][wave] sums of squares
+  const int rounds = (L.M + NWG * 4 - 1) / (NWG * 4);
 #pragma unroll 1
-  for (int m = vwg() * 4 + wave_id(); m < L.M; m += NWG * 4) {
-    f32x4 x[8];
+  for (int it = 0; it < rounds; it++) {
+    const int m = (it * 4 + q) * NWG + vwg();
+    const bool has = m < L.M;
+    const int mr = has ? m : 0;  // a pair without a row reads row 0 and stores nothing
+    f32x4 x[4];
     if (FIRST) {
 #pragma unroll
-      for (int k = 0; k < 8; k++)
-        x[k] = as_f32x4(ldb128<kCpPlain>(xin, (uint32_t)(((size_t)m * D + 4 * lane + 256 * k) * 4)));
+      for (int k = 0; k < 4; k++)
+        x[k] = as_f32x4(ldb128<kCpPlain>(xin, (uint32_t)(((size_t)mr * D + 4 * lane + 256 * k + 1024 * hh) * 4)));
     } else {
-      u32x4 xo[8], pr[NS][8];
+      u32x4 xo[4], pr[NS][4];
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
-        const int d = 4 * lane + 256 * k;
-        xo[k] = ldb128<kCpSc1>(ws, (uint32_t)(L.x + ((size_t)m * D + d) * 4));
+      for (int k = 0; k < 4; k++) {
+        const int d = 4 * lane + 256 * k + 1024 * hh;
+        xo[k] = ldb128<kCpSc1>(ws, (uint32_t)(L.x + ((size_t)mr * D + d) * 4));
 #pragma unroll
         for (int s = 0; s < NS; s++)
-          pr[s][k] = ldb128<kCpSc1>(ws, (uint32_t)(L.part + (((size_t)s * L.MP + m) * D + d) * 4));
+          pr[s][k] = ldb128<kCpSc1>(ws, (uint32_t)(L.part + (((size_t)s * L.MP + mr) * D + d) * 4));
       }
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
-        f32x4 s = as_f32x4(pr[0][k]);
+      for (int k = 0; k < 4; k++) {
+        f32x4 t = as_f32x4(pr[0][k]);
 #pragma unroll
-        for (int sp = 1; sp < NS; sp++) s += as_f32x4(pr[sp][k]);
-        x[k] = as_f32x4(xo[k]) + s;
+        for (int sp = 1; sp < NS; sp++) t += as_f32x4(pr[sp][k]);
+        x[k] = as_f32x4(xo[k]) + t;
       }
     }
     float ss = 0.f;
 #pragma unroll
-    for (int k = 0; k < 8; k++) ss += x[k][0] * x[k][0] + x[k][1] * x[k][1] + x[k][2] * x[k][2] + x[k][3] * x[k][3];
-    const float rr = rsqrtf(wave_sum(ss) / (float)D + 1e-6f);
+    for (int k = 0; k < 4; k++) ss += x[k][0] * x[k][0] + x[k][1] * x[k][1] + x[k][2] * x[k][2] + x[k][3] * x[k][3];
+    ss = wave_sum(ss);
+    if (lane == 0) red[(it & 1) * NWAVE + wv] = ss;
+    __syncthreads();
+    const float rr = rsqrtf((red[(it & 1) * NWAVE + q] + red[(it & 1) * NWAVE + q + 4]) / (float)D + 1e-6f);
+    if (!has) continue;
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int d = 4 * lane + 256 * k;
-      const f32x4 wv = *reinterpret_cast<const f32x4*>(w + d);
+    for (int k = 0; k < 4; k++) {
+      const int d = 4 * lane + 256 * k + 1024 * hh;
+      const f32x4 wv4 = *reinterpret_cast<const f32x4*>(w + d);
       f32x4 h;
 #pragma unroll
-      for (int i = 0; i < 4; i++) h[i] = x[k][i] * rr * (1.0f + wv[i]);
+      for (int i = 0; i < 4; i++) h[i] = x[k][i] * rr * (1.0f + wv4[i]);
       st_b128(ws, (uint32_t)(L.x + ((size_t)m * D + d) * 4), as_u32x4(x[k]));
       const unsigned lo = pack_bf16x2(h[0], h[1]), hi = pack_bf16x2(h[2], h[3]);
       if (!FRAG) {

@@ -1,6 +1,8 @@
-// Stage engine of the batched denoise kernels (MFMA-bound regime: M = batch x Tv tokens).
+// Stage engine of the batched denoise kernels and the prefix prefill (MFMA-bound regime: M = batch x
+// Tv tokens, or the prefix tokens).
 //
-// One cooperative launch of 256 workgroups (one per CU) x 256 threads (4 waves). The loop is a
+// One cooperative launch of 256 workgroups (one per CU) x NWAVE waves (4, or 8 where the kernel's
+// source sets FA_ENG_NWAVE; see below). The loop is a
 // fixed sequence of stages separated by grid barriers; inside a stage the workgroups take work
 // items (GEMM tiles, attention blocks, rows) round robin in an XCD-major order, so consecutive
 // items (which share a weight tile) run on the CUs of one XCD and hit that XCD's L2.

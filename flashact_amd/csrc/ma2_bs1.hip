@@ -44,11 +44,14 @@ constexpr uint32_t OFF_CTRL = 0;     // u64 seq, u32 err @8, u32 exchange parity
 constexpr uint32_t OFF_XFLAG = 1024; // [8 XCD][32 rank] u64 epochs
 constexpr uint32_t OFF_XP = kWsDataBase;  // [2 buffers][8 XCD][32 tokens][768] f32 (parity-tagged)
 constexpr uint32_t XP_BYTES = 2 * NX * TP * D * 4;
-// per-XCD block (stride XB): activations in MFMA fragment order and small fp32 intermediates
+// per-XCD block (stride XB): activations in MFMA fragment order and small fp32 intermediates.
+// X_QKV and X_QC are lane-major, in the order the attention stages read them: 16-byte group
+// (token tile tt, slot s, lane lr + 16 g4) holds dims 24 g4 + 4 (s % 6) .. + 3 of part s / 6
+// (q | k | v) of token 16 tt + lr, so each of those loads reads 1 KB contiguous.
 constexpr uint32_t X_XN = 0;                          // [32][768] bf16 fragments
-constexpr uint32_t X_QKV = X_XN + TP * D * 2;         // [32][288] f32 (q | k | v of head g, + bias)
+constexpr uint32_t X_QKV = X_XN + TP * D * 2;         // [2][18][64] f32x4 (q | k | v of head g, + bias)
 constexpr uint32_t X_ATT = X_QKV + TP * 288 * 4;      // [32][96] bf16 fragments
-constexpr uint32_t X_QC = X_ATT + TP * HD * 2;        // [32][96] f32 (+ bias)
+constexpr uint32_t X_QC = X_ATT + TP * HD * 2;        // [2][6][64] f32x4 (+ bias)
 constexpr uint32_t X_CP = X_QC + TP * HD * 4;         // [16 chunks][32][96] bf16 partials
 constexpr uint32_t X_CML = X_CP + 16 * TP * HD * 2;   // [16][32] (m, l) f32
 constexpr uint32_t X_H = X_CML + 16 * TP * 8;         // [32][384] bf16 fragments
@@ -275,8 +278,11 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int bu
 // ---- GEMM pieces -------------------------------------------------------------------------------
 // One 16-row weight tile over all 32 tokens, K = 768 split over the 4 waves (k-steps 6w..6w+5;
 // wf = this wave's weight fragments, loaded ahead). The four partial sums meet in LDS; waves 0/1
-// finish token tiles 0/1: + bias, fp32 rows [token][col0 + 4 lq + i] (row stride ld) at `out`.
-__device__ __forceinline__ void gemm16(const Params& p, const Ctx& c, const u32x4 (&wf)[6], uint32_t out, int ld,
+// finish token tiles 0/1: + bias, columns col0 + 4 lq .. + 3 (of ns 96-column parts) into the
+// lane-major layout of X_QKV / X_QC at `out` (each store instruction writes 4 runs of 256 bytes;
+// row-major [token][column] rows read back by lanes 96 bytes apart took the self attention's loads
+// through about seven 128-byte lines per kilobyte used).
+__device__ __forceinline__ void gemm16(const Params& p, const Ctx& c, const u32x4 (&wf)[6], uint32_t out, int ns,
                                        int col0, const float* bias) {
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
   u32x4 b[2][6];
@@ -298,7 +304,9 @@ __device__ __forceinline__ void gemm16(const Params& p, const Ctx& c, const u32x
     f32x4 s = (red[(0 * 2 + tt) * 64 + c.lane] + red[(1 * 2 + tt) * 64 + c.lane]) +
               (red[(2 * 2 + tt) * 64 + c.lane] + red[(3 * 2 + tt) * 64 + c.lane]);
     s += *reinterpret_cast<const f32x4*>(bias + 4 * c.lq);
-    *reinterpret_cast<f32x4*>(p.ws + c.xb + out + ((16 * tt + c.lr) * ld + col0 + 4 * c.lq) * 4) = s;
+    const int col = col0 + 4 * c.lq, j = (col % HD) >> 2;  // 4-column group j of part col / 96
+    const int slot = 6 * (col / HD) + j % 6;
+    *reinterpret_cast<f32x4*>(p.ws + c.xb + out + (((tt * 6 * ns + slot) * 64 + c.lr + 16 * (j / 6)) * 16)) = s;
   }
 }
 
@@ -337,14 +345,12 @@ __device__ __forceinline__ void stage_satt(const Params& p, const Ctx& c) {
   const bool tv = tau < p.Tv;
   float q[24], k[24], v[24];
   {
-    const int tq = tv ? tau : 0;
+    // slots 0-5 / 6-11 / 12-17 of the lane: its 24 dims of q / k / v (a wave past Tv reads tile 0;
+    // lanes of tokens past Tv stay within their own four lanes and are written as zeros below)
+    const int tt = 16 * c.w < p.Tv ? c.w : 0;
     u32x4 r[18];
 #pragma unroll
-    for (int qq = 0; qq < 6; qq++) {
-      r[qq] = ldb128<kCpSc1>(c.ws, c.xb + X_QKV + (uint32_t)((tq * 288 + 24 * g4 + 4 * qq) * 4));
-      r[6 + qq] = ldb128<kCpSc1>(c.ws, c.xb + X_QKV + (uint32_t)((tq * 288 + 96 + 24 * g4 + 4 * qq) * 4));
-      r[12 + qq] = ldb128<kCpSc1>(c.ws, c.xb + X_QKV + (uint32_t)((tq * 288 + 192 + 24 * g4 + 4 * qq) * 4));
-    }
+    for (int s = 0; s < 18; s++) r[s] = ldb128<kCpSc1>(c.ws, c.xb + X_QKV + (uint32_t)(((tt * 18 + s) * 64 + c.lane) * 16));
 #pragma unroll
     for (int qq = 0; qq < 6; qq++)
 #pragma unroll
@@ -421,10 +427,10 @@ __device__ __forceinline__ void stage_catt(const Params& p, const Ctx& c, const 
   const bool tv = tau < p.Tv;
   float q[24];
   {
-    const int tq = tv ? tau : 0;
+    const int tt = 16 * c.w < p.Tv ? c.w : 0;
     u32x4 r[6];
 #pragma unroll
-    for (int qq = 0; qq < 6; qq++) r[qq] = ldb128<kCpSc1>(c.ws, c.xb + X_QC + (uint32_t)((tq * HD + 24 * g4 + 4 * qq) * 4));
+    for (int qq = 0; qq < 6; qq++) r[qq] = ldb128<kCpSc1>(c.ws, c.xb + X_QC + (uint32_t)(((tt * 6 + qq) * 64 + c.lane) * 16));
 #pragma unroll
     for (int qq = 0; qq < 6; qq++)
 #pragma unroll
@@ -647,9 +653,10 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
       mark(p, 15, t0);
       // QKV
       if (c.r < 18)
-        gemm16(p, c, wq, X_QKV, 288, 96 * (c.r / 6) + 16 * (c.r % 6),
+        gemm16(p, c, wq, X_QKV, 3, 96 * (c.r / 6) + 16 * (c.r % 6),
                p.b_qkv + (size_t)l * QKVN + (c.r / 6) * D + HD * c.g + 16 * (c.r % 6));
       mark(p, 1, t0);
+      xarrive(c);
       u32x4 wso[3];
       {
         const bf16* W = p.w_so + (size_t)l * D * D;
@@ -657,7 +664,6 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < 3; j++) wso[j] = wfrag(W, D, row, HD * c.g + 32 * j, c.lq);
       }
-      xarrive(c);
       xwait(c);
       mark(p, 15, t0);
       // SATT
@@ -699,7 +705,7 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
       xwait(c);
       mark(p, 15, t0);
       // CQ
-      if (c.r < 6) gemm16(p, c, wc, X_QC, HD, 16 * c.r, p.b_cq + (size_t)l * D + HD * c.g + 16 * c.r);
+      if (c.r < 6) gemm16(p, c, wc, X_QC, 1, 16 * c.r, p.b_cq + (size_t)l * D + HD * c.g + 16 * c.r);
       mark(p, 5, t0);
       xarrive(c);
       xwait(c);
@@ -713,6 +719,7 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
       // COMB, with the CO weights in flight
       stage_comb(p, c);
       mark(p, 7, t0);
+      xarrive(c);
       u32x4 wco[3];
       {
         const bf16* W = p.w_co + (size_t)l * D * D;
@@ -720,7 +727,6 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < 3; j++) wco[j] = wfrag(W, D, row, HD * c.g + 32 * j, c.lq);
       }
-      xarrive(c);
       xwait(c);
       mark(p, 15, t0);
       // CO -> exchange e1
@@ -745,6 +751,7 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
       // GU, then the down weights in flight
       stage_gu(p, c, wg, p.b_gu + (size_t)l * GUN + 2 * 384 * c.g);
       mark(p, 10, t0);
+      xarrive(c);
       u32x4 wd[12];
       {
         const bf16* W = p.w_dn + (size_t)l * D * FF;
@@ -752,7 +759,6 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < 12; j++) wd[j] = wfrag(W, FF, row, 384 * c.g + 32 * j, c.lq);
       }
-      xarrive(c);
       xwait(c);
       mark(p, 15, t0);
       // DN -> exchange e2

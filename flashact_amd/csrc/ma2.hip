@@ -326,17 +326,21 @@ __device__ __forceinline__ void stage_gate(const Params& p, rsrc_t ws, int l) {
 }
 
 // ---------------------------------------------------------------- attention pieces
-// 24 consecutive columns c0[i].. of row m of the projection y (finished, or partials + bias), for
-// each of NT bases.
+// The lane's 24 of the 96 columns c0[t] .. c0[t] + 95 of row m of the projection y (finished, or
+// partials + bias), for each of NT bases: v[t][4 s + i] = column c0[t] + 16 s + 4 g4 + i (g4 = lane / 16),
+// so the four lanes of a row read 64 contiguous bytes per load (with 24 consecutive columns per lane
+// they were 96 bytes apart, and a wave's 1 KB load touched about seven 128-byte lines per KB), and
+// the RoPE partners j, j + 48 sit in elements 4 s + i, 4 s + 12 + i of one lane.
 template <int NT, bool FIX>
 __device__ __forceinline__ void load24(rsrc_t ws, const YSrc& y, int MP, int m, const int (&c0)[NT],
                                        float (&v)[NT][24]) {
+  const int g4 = lane_id() >> 4;
   int cols[6 * NT];
   f32x4 acc[6 * NT];
 #pragma unroll
   for (int t = 0; t < NT; t++)
 #pragma unroll
-    for (int q = 0; q < 6; q++) cols[6 * t + q] = c0[t] + 4 * q;
+    for (int q = 0; q < 6; q++) cols[6 * t + q] = c0[t] + 16 * q + 4 * g4;
   if (FIX) {
     u32x4 r[6 * NT];
 #pragma unroll
@@ -357,7 +361,7 @@ __device__ __forceinline__ void load24(rsrc_t ws, const YSrc& y, int MP, int m, 
 }
 
 // Self attention of (sample b, head h) over its Tv action tokens. Wave w prepares tokens
-// 16w..16w+15 (lane: token 16w + l%16, dims 24 (l/16) ..+23) into the LDS Q/K/V^T fragments
+// 16w..16w+15 (lane: token 16w + l%16, dims 16 s + 4 (l/16) + i, s < 6, i < 4) into the LDS Q/K/V^T fragments
 // (zeros past Tv), then attends with query tile w.
 constexpr uint32_t S_Q = 0, S_K = 12 * 1024, S_V = 24 * 1024;
 
@@ -373,7 +377,7 @@ __device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, const YSr
     const int m = b * p.Tv + (tv ? tau : 0);
     float qkv[3][24];
     {
-      const int c0 = HD * h + 24 * g4;
+      const int c0 = HD * h;
       const int cs[3] = {c0, D + c0, 2 * D + c0};
       load24<3, FIX>(ws, y, L.MP, m, cs, qkv);
     }
@@ -382,39 +386,43 @@ __device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, const YSr
     float (&v)[24] = qkv[2];
     rms96(q);
     rms96(k);
-    // RoPE on split-half pairs (j, j + 48): lanes g4 = 0, 1 hold the low halves, g4 ^ 2 the partners
-    const bool lo = g4 < 2;
-    const int j0 = 24 * (g4 & 1);
+    // RoPE on split-half pairs (j, j + 48) = elements (4 s + i, 4 s + 12 + i) of the lane, s < 3
+    const float* rc = p.rope_cos + (tv ? tau : 0) * 48;
+    const float* rs = p.rope_sin + (tv ? tau : 0) * 48;
 #pragma unroll
-    for (int i = 0; i < 24; i++) {
-      const LanePair sq = swap32(as_u32(q[i]), as_u32(q[i])), sk = swap32(as_u32(k[i]), as_u32(k[i]));
-      const float qo = as_f32(lo ? sq.hi : sq.lo), ko = as_f32(lo ? sk.hi : sk.lo);  // lane ^ 32
-      const float c = p.rope_cos[(tv ? tau : 0) * 48 + j0 + i], sn = p.rope_sin[(tv ? tau : 0) * 48 + j0 + i];
-      q[i] = lo ? q[i] * c - qo * sn : qo * sn + q[i] * c;
-      k[i] = lo ? k[i] * c - ko * sn : ko * sn + k[i] * c;
+    for (int s = 0; s < 3; s++) {
+      const f32x4 c4 = *reinterpret_cast<const f32x4*>(rc + 16 * s + 4 * g4);
+      const f32x4 s4 = *reinterpret_cast<const f32x4*>(rs + 16 * s + 4 * g4);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int a = 4 * s + i, bb = a + 12;
+        const float q0 = q[a], q1 = q[bb], k0 = k[a], k1 = k[bb];
+        q[a] = q0 * c4[i] - q1 * s4[i];
+        q[bb] = q0 * s4[i] + q1 * c4[i];
+        k[a] = k0 * c4[i] - k1 * s4[i];
+        k[bb] = k0 * s4[i] + k1 * c4[i];
+      }
     }
     __syncthreads();  // the previous item's readers are done with LDS
     unsigned short* lq16 = reinterpret_cast<unsigned short*>(lds);
-    // q and k rows: the lane's 24 dims are three whole 8-dim fragment slots (16-byte writes); V^T
+    // q and k rows: each 4-dim group of the lane is half an 8-dim fragment slot (8-byte writes); V^T
     // is transposed, one element per write
     const uint32_t kr = kperm_row(tau);
 #pragma unroll
-    for (int sl = 0; sl < 3; sl++) {
-      const int d = 24 * g4 + 8 * sl;
-      u32x4 qs, ks;
+    for (int s = 0; s < 6; s++) {
+      const int d = 16 * s + 4 * g4;
+      const u32x2 qs = tv ? u32x2{pack_bf16x2(q[4 * s], q[4 * s + 1]), pack_bf16x2(q[4 * s + 2], q[4 * s + 3])} : u32x2{0u, 0u};
+      const u32x2 ks = tv ? u32x2{pack_bf16x2(k[4 * s], k[4 * s + 1]), pack_bf16x2(k[4 * s + 2], k[4 * s + 3])} : u32x2{0u, 0u};
+      *reinterpret_cast<u32x2*>(lds + S_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
+      *reinterpret_cast<u32x2*>(lds + S_K + ((kr >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(kr, d)) = ks;
+    }
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        qs[e] = tv ? pack_bf16x2(q[8 * sl + 2 * e], q[8 * sl + 2 * e + 1]) : 0u;
-        ks[e] = tv ? pack_bf16x2(k[8 * sl + 2 * e], k[8 * sl + 2 * e + 1]) : 0u;
+    for (int s = 0; s < 6; s++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int d = 16 * s + 4 * g4 + i;
+        lq16[(S_V + ((d >> 4) * 2 + (tau >> 5)) * 1024 + frag_pos(d, tau)) >> 1] = tv ? bf16_bits(v[4 * s + i]) : 0;
       }
-      *reinterpret_cast<u32x4*>(lds + S_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
-      *reinterpret_cast<u32x4*>(lds + S_K + ((kr >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(kr, d)) = ks;
-    }
-#pragma unroll
-    for (int i = 0; i < 24; i++) {
-      const int d = 24 * g4 + i;
-      lq16[(S_V + ((d >> 4) * 2 + (tau >> 5)) * 1024 + frag_pos(d, tau)) >> 1] = tv ? bf16_bits(v[i]) : 0;
-    }
     __syncthreads();
     if (16 * w < p.Tv) {
       u32x4 qf[3];
@@ -486,18 +494,16 @@ __device__ __forceinline__ void stage_catt(const Params& p, rsrc_t ws, int l, co
       const bool tv = tau < p.Tv;
       float qq[1][24];
       {
-        const int cs[1] = {HD * h + 24 * g4};
+        const int cs[1] = {HD * h};
         load24<1, FIX>(ws, y, L.MP, b * p.Tv + (tv ? tau : 0), cs, qq);
       }
       float (&q)[24] = qq[0];
       rms96(q);
 #pragma unroll
-      for (int sl = 0; sl < 3; sl++) {  // the lane's 24 dims are three whole 8-dim fragment slots
-        const int d = 24 * g4 + 8 * sl;
-        u32x4 qs;
-#pragma unroll
-        for (int e = 0; e < 4; e++) qs[e] = tv ? pack_bf16x2(q[8 * sl + 2 * e], q[8 * sl + 2 * e + 1]) : 0u;
-        *reinterpret_cast<u32x4*>(lds + cb + C_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
+      for (int s = 0; s < 6; s++) {  // element 4 s + i = dim 16 s + 4 g4 + i: half a fragment slot each
+        const int d = 16 * s + 4 * g4;
+        const u32x2 qs = tv ? u32x2{pack_bf16x2(q[4 * s], q[4 * s + 1]), pack_bf16x2(q[4 * s + 2], q[4 * s + 3])} : u32x2{0u, 0u};
+        *reinterpret_cast<u32x2*>(lds + cb + C_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
       }
     }
     unsigned vmask[4][4];

@@ -46,8 +46,9 @@ constexpr uint32_t OFF_XP = kWsDataBase;  // [2 buffers][8 XCD][32 tokens][768] 
 constexpr uint32_t XP_BYTES = 2 * NX * TP * D * 4;
 // per-XCD block (stride XB): activations in MFMA fragment order and small fp32 intermediates.
 // X_QKV and X_QC are lane-major, in the order the attention stages read them: 16-byte group
-// (token tile tt, slot s, lane lr + 16 g4) holds dims 24 g4 + 4 (s % 6) .. + 3 of part s / 6
-// (q | k | v) of token 16 tt + lr, so each of those loads reads 1 KB contiguous.
+// (token tile tt, slot s, lane lr + 16 g4) holds dims 16 (s % 6) + 4 g4 .. + 3 of part s / 6
+// (q | k | v) of token 16 tt + lr, so each of those loads reads 1 KB contiguous, and the RoPE
+// partners j, j + 48 sit in slots s, s + 3 of one lane.
 constexpr uint32_t X_XN = 0;                          // [32][768] bf16 fragments
 constexpr uint32_t X_QKV = X_XN + TP * D * 2;         // [2][18][64] f32x4 (q | k | v of head g, + bias)
 constexpr uint32_t X_ATT = X_QKV + TP * 288 * 4;      // [32][96] bf16 fragments
@@ -305,8 +306,8 @@ __device__ __forceinline__ void gemm16(const Params& p, const Ctx& c, const u32x
               (red[(2 * 2 + tt) * 64 + c.lane] + red[(3 * 2 + tt) * 64 + c.lane]);
     s += *reinterpret_cast<const f32x4*>(bias + 4 * c.lq);
     const int col = col0 + 4 * c.lq, j = (col % HD) >> 2;  // 4-column group j of part col / 96
-    const int slot = 6 * (col / HD) + j % 6;
-    *reinterpret_cast<f32x4*>(p.ws + c.xb + out + (((tt * 6 * ns + slot) * 64 + c.lr + 16 * (j / 6)) * 16)) = s;
+    const int slot = 6 * (col / HD) + (j >> 2);
+    *reinterpret_cast<f32x4*>(p.ws + c.xb + out + (((tt * 6 * ns + slot) * 64 + c.lr + 16 * (j & 3)) * 16)) = s;
   }
 }
 
@@ -345,8 +346,9 @@ __device__ __forceinline__ void stage_satt(const Params& p, const Ctx& c) {
   const bool tv = tau < p.Tv;
   float q[24], k[24], v[24];
   {
-    // slots 0-5 / 6-11 / 12-17 of the lane: its 24 dims of q / k / v (a wave past Tv reads tile 0;
-    // lanes of tokens past Tv stay within their own four lanes and are written as zeros below)
+    // slots 0-5 / 6-11 / 12-17 of the lane: q / k / v, element 4 s + i = dim 16 s + 4 g4 + i (a wave
+    // past Tv reads tile 0; lanes of tokens past Tv stay within their own four lanes and are
+    // written as zeros below)
     const int tt = 16 * c.w < p.Tv ? c.w : 0;
     u32x4 r[18];
 #pragma unroll
@@ -362,39 +364,40 @@ __device__ __forceinline__ void stage_satt(const Params& p, const Ctx& c) {
   }
   rms96(q);
   rms96(k);
-  const bool lo = g4 < 2;
-  const int j0 = 24 * (g4 & 1);
+  // RoPE on split-half pairs (j, j + 48) = elements (4 s + i, 4 s + 12 + i) of the lane, s < 3
+  const float* rope = reinterpret_cast<const float*>(lds + L_ROPE) + (tv ? tau : 0) * 48;  // staged by the prologue
 #pragma unroll
-  for (int i = 0; i < 24; i++) {
-    const LanePair sq = swap32(as_u32(q[i]), as_u32(q[i])), sk = swap32(as_u32(k[i]), as_u32(k[i]));
-    const float qo = as_f32(lo ? sq.hi : sq.lo), ko = as_f32(lo ? sk.hi : sk.lo);  // lane ^ 32
-    const float* rope = reinterpret_cast<const float*>(lds + L_ROPE);  // staged by the prologue
-    const float cs = rope[(tv ? tau : 0) * 48 + j0 + i], sn = rope[TP * 48 + (tv ? tau : 0) * 48 + j0 + i];
-    q[i] = lo ? q[i] * cs - qo * sn : qo * sn + q[i] * cs;
-    k[i] = lo ? k[i] * cs - ko * sn : ko * sn + k[i] * cs;
-  }
+  for (int s = 0; s < 3; s++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int j = 16 * s + 4 * g4 + i, a = 4 * s + i, b = a + 12;
+      const float cs = rope[j], sn = rope[TP * 48 + j];
+      const float q0 = q[a], q1 = q[b], k0 = k[a], k1 = k[b];
+      q[a] = q0 * cs - q1 * sn;
+      q[b] = q0 * sn + q1 * cs;
+      k[a] = k0 * cs - k1 * sn;
+      k[b] = k0 * sn + k1 * cs;
+    }
   constexpr uint32_t SQ = 0, SK = 12 * 1024, SV = 24 * 1024;
-  // q and k rows: the lane's 24 dims are three whole 8-dim slots of the fragments (16-byte writes);
+  // q and k rows: each 4-dim group of the lane is half an 8-dim fragment slot (8-byte writes);
   // V^T is transposed, one element per write (pairing neighbouring tokens through DPP was slower)
   const uint32_t kr = kperm_row(tau);
 #pragma unroll
-  for (int sl = 0; sl < 3; sl++) {
-    const int d = 24 * g4 + 8 * sl;
-    u32x4 qs, ks;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      qs[e] = tv ? pack_bf16x2(q[8 * sl + 2 * e], q[8 * sl + 2 * e + 1]) : 0u;
-      ks[e] = tv ? pack_bf16x2(k[8 * sl + 2 * e], k[8 * sl + 2 * e + 1]) : 0u;
-    }
-    *reinterpret_cast<u32x4*>(lds + L_ATT + SQ + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
-    *reinterpret_cast<u32x4*>(lds + L_ATT + SK + ((kr >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(kr, d)) = ks;
+  for (int s = 0; s < 6; s++) {
+    const int d = 16 * s + 4 * g4;
+    const u32x2 qs = tv ? u32x2{pack_bf16x2(q[4 * s], q[4 * s + 1]), pack_bf16x2(q[4 * s + 2], q[4 * s + 3])} : u32x2{0u, 0u};
+    const u32x2 ks = tv ? u32x2{pack_bf16x2(k[4 * s], k[4 * s + 1]), pack_bf16x2(k[4 * s + 2], k[4 * s + 3])} : u32x2{0u, 0u};
+    *reinterpret_cast<u32x2*>(lds + L_ATT + SQ + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
+    *reinterpret_cast<u32x2*>(lds + L_ATT + SK + ((kr >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(kr, d)) = ks;
   }
   unsigned short* l16 = reinterpret_cast<unsigned short*>(lds + L_ATT);
 #pragma unroll
-  for (int i = 0; i < 24; i++) {
-    const int d = 24 * g4 + i;
-    l16[(SV + ((d >> 4) * 2 + (tau >> 5)) * 1024 + frag_pos(d, tau)) >> 1] = tv ? bf16_bits(v[i]) : 0;
-  }
+  for (int s = 0; s < 6; s++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int d = 16 * s + 4 * g4 + i;
+      l16[(SV + ((d >> 4) * 2 + (tau >> 5)) * 1024 + frag_pos(d, tau)) >> 1] = tv ? bf16_bits(v[4 * s + i]) : 0;
+    }
   __syncthreads();
   if (16 * c.w < p.Tv) {
     u32x4 qf[3];
@@ -438,12 +441,10 @@ __device__ __forceinline__ void stage_catt(const Params& p, const Ctx& c, const 
   }
   rms96(q);
 #pragma unroll
-  for (int sl = 0; sl < 3; sl++) {  // the lane's 24 dims are three whole 8-dim fragment slots
-    const int d = 24 * g4 + 8 * sl;
-    u32x4 qs;
-#pragma unroll
-    for (int e = 0; e < 4; e++) qs[e] = tv ? pack_bf16x2(q[8 * sl + 2 * e], q[8 * sl + 2 * e + 1]) : 0u;
-    *reinterpret_cast<u32x4*>(lds + L_ATT + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
+  for (int s = 0; s < 6; s++) {  // element 4 s + i = dim 16 s + 4 g4 + i: half a fragment slot each
+    const int d = 16 * s + 4 * g4;
+    const u32x2 qs = tv ? u32x2{pack_bf16x2(q[4 * s], q[4 * s + 1]), pack_bf16x2(q[4 * s + 2], q[4 * s + 3])} : u32x2{0u, 0u};
+    *reinterpret_cast<u32x2*>(lds + L_ATT + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
   }
   __syncthreads();
   if (16 * c.w >= p.Tv) return;

@@ -408,11 +408,12 @@ __device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, const YSr
     // q and k rows: each 4-dim group of the lane is half an 8-dim fragment slot (8-byte writes); V^T
     // is transposed, one element per write
     const uint32_t kr = kperm_row(tau);
+    const unsigned keep = keep_mask(tv);
 #pragma unroll
     for (int s = 0; s < 6; s++) {
       const int d = 16 * s + 4 * g4;
-      const u32x2 qs = tv ? u32x2{pack_bf16x2(q[4 * s], q[4 * s + 1]), pack_bf16x2(q[4 * s + 2], q[4 * s + 3])} : u32x2{0u, 0u};
-      const u32x2 ks = tv ? u32x2{pack_bf16x2(k[4 * s], k[4 * s + 1]), pack_bf16x2(k[4 * s + 2], k[4 * s + 3])} : u32x2{0u, 0u};
+      const u32x2 qs = pack4(q, s, keep);
+      const u32x2 ks = pack4(k, s, keep);
       *reinterpret_cast<u32x2*>(lds + S_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
       *reinterpret_cast<u32x2*>(lds + S_K + ((kr >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(kr, d)) = ks;
     }
@@ -421,7 +422,7 @@ __device__ __forceinline__ void stage_satt(const Params& p, rsrc_t ws, const YSr
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int d = 16 * s + 4 * g4 + i;
-        lq16[(S_V + ((d >> 4) * 2 + (tau >> 5)) * 1024 + frag_pos(d, tau)) >> 1] = tv ? bf16_bits(v[4 * s + i]) : 0;
+        lq16[(S_V + ((d >> 4) * 2 + (tau >> 5)) * 1024 + frag_pos(d, tau)) >> 1] = (unsigned short)(bf16_bits(v[4 * s + i]) & keep);
       }
     __syncthreads();
     if (16 * w < p.Tv) {
@@ -499,10 +500,11 @@ __device__ __forceinline__ void stage_catt(const Params& p, rsrc_t ws, int l, co
       }
       float (&q)[24] = qq[0];
       rms96(q);
+      const unsigned keep = keep_mask(tv);
 #pragma unroll
       for (int s = 0; s < 6; s++) {  // element 4 s + i = dim 16 s + 4 g4 + i: half a fragment slot each
         const int d = 16 * s + 4 * g4;
-        const u32x2 qs = tv ? u32x2{pack_bf16x2(q[4 * s], q[4 * s + 1]), pack_bf16x2(q[4 * s + 2], q[4 * s + 3])} : u32x2{0u, 0u};
+        const u32x2 qs = pack4(q, s, keep);
         *reinterpret_cast<u32x2*>(lds + cb + C_Q + ((tau >> 4) * 3 + (d >> 5)) * 1024 + frag_pos(tau, d)) = qs;
       }
     }

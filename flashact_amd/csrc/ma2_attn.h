@@ -87,6 +87,20 @@ __device__ __forceinline__ void attend(const u32x4 (&qf)[3], uint32_t kbase, uin
   psum = ps;
 }
 
+// All ones for a valid token, zero otherwise, hidden from the optimizer so that `x & mask` stays a
+// bitwise AND. Written as `valid ? f(x) : 0`, the selects became branches around f, and the
+// compiler's wait analysis (which does not pair branches) then waited at the top of each branch for
+// every LDS write issued before it: about a dozen LDS round trips in a row in the self attention.
+__device__ __forceinline__ unsigned keep_mask(bool valid) {
+  unsigned m = valid ? 0xffffffffu : 0u;
+  asm volatile("" : "+v"(m));
+  return m;
+}
+// Elements 4 s .. 4 s + 3 of v as two bf16 pairs, ANDed with a keep_mask.
+__device__ __forceinline__ u32x2 pack4(const float (&v)[24], int s, unsigned keep) {
+  return u32x2{pack_bf16x2(v[4 * s], v[4 * s + 1]) & keep, pack_bf16x2(v[4 * s + 2], v[4 * s + 3]) & keep};
+}
+
 // RMS over the 96 dims of a head held by 4 lanes (xor 16, 32) as 24 values each.
 __device__ __forceinline__ void rms96(float (&v)[24]) {
   float ss = 0.f;

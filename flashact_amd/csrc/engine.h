@@ -314,7 +314,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
     // a store instruction writes whole lines (two 512-byte rows of fp32 partials, or eight 128-byte
     // rows of bf16 h) instead of 16 B into each of 16 rows.
     constexpr int OB = Epi::kRowBytes, RB = S::BN / 4 * OB, RP = RB + 16;
-    static_assert(OB == 4 || OB == 16, "4 or 16 output bytes per 4 features");
+    static_assert(OB == 4 || OB == 8 || OB == 16, "4, 8 or 16 output bytes per 4 features");
     static_assert(S::BM * RP <= S::LDS, "the staged tile fits the ring");
     static_assert(RB % 16 == 0 && NTHR % (RB / 16) == 0, "whole rows per pass");
 #pragma unroll
@@ -326,6 +326,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
         const uint32_t a = (uint32_t)(ml * RP + (nl >> 2) * OB);
         if constexpr (OB == 16)
           *reinterpret_cast<u32x4*>(lds + a) = v;
+        else if constexpr (OB == 8)
+          *reinterpret_cast<u32x2*>(lds + a) = u32x2{v[0], v[1]};
         else
           *reinterpret_cast<unsigned*>(lds + a) = v[0];
       }
@@ -351,6 +353,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
           const uint32_t o = epi.row_off(m0 + ml, n0) + (uint32_t)((nl >> 2) * OB);
           if constexpr (OB == 16)
             st_b128(epi.ws, o, v);
+          else if constexpr (OB == 8)
+            st_b64(epi.ws, o, u32x2{v[0], v[1]});
           else
             st_b32(epi.ws, o, v[0]);
         }

@@ -12,12 +12,12 @@
 //   ATT  per (sample, 128-key chunk, 16 query tiles): every query row against the chunk's keys
 //        (the prefix attends to itself without a mask), online softmax -> partial O + (m, l)
 //   COMB combine of the key chunks -> attn [M x 2048]
-//   O    [M x 2048] = attn Wo^T, K split 2 ways -> fp32 partials
+//   O    [M x 2048] = attn Wo^T, K split 2 ways -> bf16 partials
 // O, GU and DN read their token operand (attn, xn after N2, h) in MFMA fragment order.
 //   N2   x += sum(partials); xn = rms(x) (1 + w_post), written in MFMA fragment order
 //   GU   [M x 32768] = xn Wgu^T (gate/up rows interleaved, 512 x 128 tiles) -> h = gelu_tanh(g) u
 //        [M x 16384], fragment order
-//   DN   [M x 2048] = h Wdn^T (512 x 128 tiles), K split 8 ways -> fp32 partials
+//   DN   [M x 2048] = h Wdn^T (512 x 128 tiles), K split 8 ways -> bf16 partials
 // The last layer stops after QKV: its attention and MLP outputs reach no cache entry.
 // Two waves per SIMD (8 per workgroup): the tall MLP tiles keep the MFMA pipe busy about 1.4x as long
 // as one wave per SIMD can, at a budget of 256 registers per lane in every stage.
@@ -104,23 +104,29 @@ struct EpiGeluF {
   }
 };
 
-struct EpiPartT {  // fp32 partial sums [split][MP][2048] from the tall tile: 16 bytes per lane and block
+// bf16 partial sums [split][MP][2048] of the down projection (tall tile, 8 bytes per lane and block).
+// The next N1 reads all eight of them with the residual x: as fp32 they were 63 MB of the stage's
+// 83 MB per layer at Lp = 968 (N1 and this stage's stores both bandwidth-bound). Each partial is
+// rounded once to bf16 before the fp32 sum: the precision of the reference's bf16 backbone, whose
+// residual stream itself is bf16; the range is fp32's.
+struct EpiPartB {
   rsrc_t ws;
   uint32_t off;
   int MP, split;
   __device__ void operator()(int n, int m, f32x4 v) const {
-    st_b128(ws, off + (uint32_t)((((size_t)split * MP + m) * D + n) * 4), as_u32x4(v));
+    st_b64(ws, off + (uint32_t)((((size_t)split * MP + m) * D + n) * 2),
+           u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])});
   }
 };
 
-struct EpiPart : NoPre {  // fp32 partial sums [split][MP][2048]
-  static constexpr int kRowBytes = 16;
+struct EpiPart : NoPre {  // bf16 partial sums [split][MP][2048] of the O projection (as EpiPartB)
+  static constexpr int kRowBytes = 8;
   static constexpr bool kStaged = true;
   rsrc_t ws;
   uint32_t off;
   int MP, split;
-  __device__ u32x4 pack(int, f32x4 v) const { return as_u32x4(v); }
-  __device__ uint32_t row_off(int m, int n0) const { return off + (uint32_t)((((size_t)split * MP + m) * D + n0) * 4); }
+  __device__ u32x4 pack(int, f32x4 v) const { return u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), 0u, 0u}; }
+  __device__ uint32_t row_off(int m, int n0) const { return off + (uint32_t)((((size_t)split * MP + m) * D + n0) * 2); }
 };
 
 // A token row per wave pair (q, q + 4) of a workgroup (q < 4): half hh = wave / 4 of the pair takes
@@ -129,12 +135,12 @@ struct EpiPart : NoPre {  // fp32 partial sums [split][MP][2048]
 // needed two rounds of loads for eight down partials: N1 16.2 µs per layer.) Rows go pair-major,
 // row m on workgroup m % 256, so they spread over every CU; every wave runs the same number of rounds,
 // since the exchange is a workgroup barrier. FIRST: x = the prefix hidden states; otherwise x += the
-// sum of the NS K-split partials (in split order). Then xn = rms(x) (1 + w), with FRAG in MFMA fragment
+// sum of the NS K-split partials (in split order; PB: bf16 partials, else fp32). Then xn = rms(x) (1 + w), with FRAG in MFMA fragment
 // order (columns c..c+7 of token m, c % 8 = 0: the 16-byte slot (k-quarter (c % 32) / 8, token m % 16)
 // of fragment (m / 16, c / 32)), else row-major [M][2048]. The QKV GEMM after N1 reads the row-major
 // form: fragment slots written 16 bytes at a time by the waves of 16 different tokens took N1 from
 // 10.0 to 12.8 µs per layer here, more than the fragment-order copies save in the GEMM.
-template <bool FIRST, int NS, bool FRAG>
+template <bool FIRST, int NS, bool FRAG, bool PB = false>
 __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xin, const float* w) {
   static_assert(NWAVE == 8, "a row per wave pair");
   const Layout& L = p.L;
@@ -152,20 +158,43 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xi
       for (int k = 0; k < 4; k++)
         x[k] = as_f32x4(ldb128<kCpPlain>(xin, (uint32_t)(((size_t)mr * D + 4 * lane + 256 * k + 1024 * hh) * 4)));
     } else {
-      u32x4 xo[4], pr[NS][4];
+      u32x4 xo[4];
+      f32x4 pf[NS][4];
+      if constexpr (PB) {
+        u32x2 pr[NS][4];
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int d = 4 * lane + 256 * k + 1024 * hh;
-        xo[k] = ldb128<kCpSc1>(ws, (uint32_t)(L.x + ((size_t)mr * D + d) * 4));
+        for (int k = 0; k < 4; k++) {
+          const int d = 4 * lane + 256 * k + 1024 * hh;
+          xo[k] = ldb128<kCpSc1>(ws, (uint32_t)(L.x + ((size_t)mr * D + d) * 4));
+#pragma unroll
+          for (int s = 0; s < NS; s++)
+            pr[s][k] = ldb64<kCpSc1>(ws, (uint32_t)(L.part + (((size_t)s * L.MP + mr) * D + d) * 2));
+        }
 #pragma unroll
         for (int s = 0; s < NS; s++)
-          pr[s][k] = ldb128<kCpSc1>(ws, (uint32_t)(L.part + (((size_t)s * L.MP + mr) * D + d) * 4));
+#pragma unroll
+          for (int k = 0; k < 4; k++)
+            pf[s][k] = f32x4{bf_lo(pr[s][k][0]), bf_hi(pr[s][k][0]), bf_lo(pr[s][k][1]), bf_hi(pr[s][k][1])};
+      } else {
+        u32x4 pr[NS][4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int d = 4 * lane + 256 * k + 1024 * hh;
+          xo[k] = ldb128<kCpSc1>(ws, (uint32_t)(L.x + ((size_t)mr * D + d) * 4));
+#pragma unroll
+          for (int s = 0; s < NS; s++)
+            pr[s][k] = ldb128<kCpSc1>(ws, (uint32_t)(L.part + (((size_t)s * L.MP + mr) * D + d) * 4));
+        }
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+          for (int k = 0; k < 4; k++) pf[s][k] = as_f32x4(pr[s][k]);
       }
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        f32x4 t = as_f32x4(pr[0][k]);
+        f32x4 t = pf[0][k];
 #pragma unroll
-        for (int sp = 1; sp < NS; sp++) t += as_f32x4(pr[sp][k]);
+        for (int sp = 1; sp < NS; sp++) t += pf[sp][k];
         x[k] = as_f32x4(xo[k]) + t;
       }
     }
@@ -241,7 +270,7 @@ __global__ void __launch_bounds__(NTHR, 1) prefill_kernel(Params p) {
     if (l == 0)
       stage_norm<true, 1, false>(p, ws, xin, p.ln_in);
     else
-      stage_norm<false, KS_DN, false>(p, ws, xin, p.ln_in + (size_t)l * D);
+      stage_norm<false, KS_DN, false, true>(p, ws, xin, p.ln_in + (size_t)l * D);
     mark(p, 0, t0);
     grid_sync(grid);
     mark(p, 9, t0);
@@ -270,7 +299,7 @@ __global__ void __launch_bounds__(NTHR, 1) prefill_kernel(Params p) {
     mark(p, 4, t0);
     grid_sync(grid);
     mark(p, 9, t0);
-    stage_norm<false, KS_O, true>(p, ws, xin, p.ln_post + (size_t)l * D);
+    stage_norm<false, KS_O, true, true>(p, ws, xin, p.ln_post + (size_t)l * D);
     mark(p, 5, t0);
     grid_sync(grid);
     mark(p, 9, t0);
@@ -283,7 +312,7 @@ __global__ void __launch_bounds__(NTHR, 1) prefill_kernel(Params p) {
     grid_sync(grid);
     mark(p, 9, t0);
     {
-      EpiPartT e{ws, (uint32_t)L.part, L.MP, 0};
+      EpiPartB e{ws, (uint32_t)L.part, L.MP, 0};
       ghf.W = p.wdn + (size_t)l * D * FF;
       gemm_stage_tall(ghf, D, FF, KS_DN, e);
     }

@@ -311,8 +311,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
   if constexpr (Epi::kRowBytes > 0 && Epi::kStaged) {
     // Staged row-out epilogue: every lane packs its 4 features into OB bytes, the tile goes through
     // LDS (the ring is free), and each thread then stores 16 contiguous bytes of an output row, so
-    // a store instruction writes whole lines (two 512-byte rows of fp32 partials, or eight 128-byte
-    // rows of bf16 h) instead of 16 B into each of 16 rows.
+    // a store instruction writes whole lines (two 512-byte rows of fp32 partials, four 256-byte rows
+    // of bf16 partials, or eight 128-byte rows of bf16 h) instead of 16 B into each of 16 rows.
     constexpr int OB = Epi::kRowBytes, RB = S::BN / 4 * OB, RP = RB + 16;
     static_assert(OB == 4 || OB == 8 || OB == 16, "4, 8 or 16 output bytes per 4 features");
     static_assert(S::BM * RP <= S::LDS, "the staged tile fits the ring");
@@ -341,7 +341,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
     }
     __syncthreads();  // the staged tile is read before the next tile's copies land
   } else if constexpr (Epi::kRowBytes > 0) {
-    // the same bytes stored in place: 16 B (or 4 B) into each of the 16 rows of an instruction
+    // the same bytes stored in place: 16, 8 or 4 B into each of the 16 rows of an instruction
     constexpr int OB = Epi::kRowBytes;
 #pragma unroll
     for (int j = 0; j < WN; j++)
@@ -370,8 +370,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
   }
 }
 
-// Epilogue base for epilogues without per-element inputs. An epilogue that sets kRowBytes (4 or
-// 16: output bytes per 4 consecutive features) instead provides pack(n, v) (the bytes of features
+// Epilogue base for epilogues without per-element inputs. An epilogue that sets kRowBytes (4, 8
+// or 16: output bytes per 4 consecutive features) instead provides pack(n, v) (the bytes of features
 // n..n+3, in the low words) and row_off(m, n0) (byte offset in `ws` of row m's features from the
 // tile's first feature n0); with kStaged, gemm_tile writes its rows whole through LDS (measured:
 // MolmoAct2 batch 16 46.3 -> 45.1 ms, prefill 6.71 -> 6.64 ms; the batch-16 pi0.5 kernel, whose

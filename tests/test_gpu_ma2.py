@@ -38,8 +38,11 @@ def test_ma2_config4_bs1(gpu):
     _check(C.make_case(NL=36, Lk=493, Tv=30, S=10), gpu)
 
 
+# Batch 1 runs the XCD-local kernel up to Tv = 32 and Lk = 512: (1, 512, 32) fills every token lane
+# and context rank; (1, 65, 17) leaves one token in the second token tile and a ragged key chunk.
 @pytest.mark.parametrize("B,Lk,Tv,S,adim", [(1, 1, 1, 2, 6), (2, 700, 64, 1, 32), (3, 37, 17, 2, 5),
-                                            (1, 128, 16, 1, 6), (2, 129, 33, 1, 1)])
+                                            (1, 128, 16, 1, 6), (2, 129, 33, 1, 1), (1, 512, 32, 2, 6),
+                                            (1, 65, 17, 2, 7)])
 def test_ma2_edge_shapes(gpu, B, Lk, Tv, S, adim):
     _check(C.make_case(NL=2, Lk=Lk, Tv=Tv, S=S, adim=adim, batch=B, seed=Lk + Tv), gpu)
 

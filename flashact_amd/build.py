@@ -3,6 +3,7 @@ from __future__ import annotations
 
 import concurrent.futures
 import glob
+import json
 import os
 import re
 import subprocess
@@ -24,6 +25,40 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-kernel register budget: the build fails when a kernel spills more VGPRs (or uses more scratch
+# bytes per lane) than listed here, so a change that pushes a hot loop into scratch is caught at
+# build time. Kernels not listed must not spill at all.
+RESOURCE_BUDGET = os.path.join(HERE, "resource_budget.json")
+RESOURCE_REPORT = os.path.join(LIB_DIR, "resource_usage.json")
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|VGPRs Spill|SGPRs Spill):\s+(\S+)")
+
+
+def parse_resource_usage(text: str) -> dict:
+    """{kernel symbol: {"vgpr", "agpr", "scratch", "vgpr_spill", "sgpr_spill"}} from the compiler's
+    -Rpass-analysis=kernel-resource-usage remarks."""
+    keys = {"VGPRs": "vgpr", "AGPRs": "agpr", "ScratchSize [bytes/lane]": "scratch", "VGPRs Spill": "vgpr_spill",
+            "SGPRs Spill": "sgpr_spill"}
+    out, cur = {}, None
+    for m in _REMARK.finditer(text):
+        k, v = m.group(1), m.group(2)
+        if k == "Function Name":
+            cur = out.setdefault(v, {})
+        elif cur is not None:
+            cur[keys[k]] = int(v)
+    return out
+
+
+def check_resources(usage: dict) -> list:
+    budget = json.load(open(RESOURCE_BUDGET)) if os.path.exists(RESOURCE_BUDGET) else {}
+    bad = []
+    for name, u in sorted(usage.items()):
+        b = budget.get(name, {"vgpr_spill": 0, "scratch": 0})
+        if u.get("vgpr_spill", 0) > b["vgpr_spill"] or u.get("scratch", 0) > b["scratch"]:
+            bad.append(f"{name}: {u.get('vgpr_spill', 0)} spilled VGPRs / {u.get('scratch', 0)} B scratch per lane "
+                       f"> budget {b['vgpr_spill']} / {b['scratch']}")
+    return bad
+
+
 # hipcc (ROCm 7.2) evaluates __builtin_bit_cast(T, v[i]) on an ext_vector element as a cast of
 # element 0; kernels use as_f32/as_u32 (fa_device.h) instead, and the build rejects the direct form.
 BAD_BITCAST = re.compile(r"__builtin_bit_cast\(\s*[\w:]+\s*,\s*[^(),]*\[")
@@ -42,7 +77,8 @@ def sources():
 
 
 def _compile(hipcc: str, src: str, obj: str) -> tuple[str, int, str]:
-    cmd = [hipcc, *HIPCC_FLAGS, "-c", "-I", os.path.join(ROOT, "include"), src, "-o", obj]
+    cmd = [hipcc, *HIPCC_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", "-I", os.path.join(ROOT, "include"),
+           src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in l)
     return src, res.returncode, out
@@ -60,11 +96,23 @@ def build(verbose: bool = False) -> str:
     jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16))
     with concurrent.futures.ThreadPoolExecutor(jobs) as ex:
         results = list(ex.map(lambda so: _compile(hipcc, *so), zip(srcs, objs)))
+    usage = {}
     for src, rc, out in results:
         if rc != 0:
             raise RuntimeError(f"hipcc failed on {src} ({rc}):\n{out}")
-        if verbose and out.strip():
-            print(out, file=sys.stderr)
+        usage.update(parse_resource_usage(out))
+        rest = "\n".join(l for l in out.splitlines() if "kernel-resource-usage" not in l and not l.startswith(" "))
+        if verbose and rest.strip():
+            print(rest, file=sys.stderr)
+    with open(RESOURCE_REPORT, "w") as f:
+        json.dump(usage, f, indent=1, sort_keys=True)
+    if verbose:
+        for name, u in sorted(usage.items()):
+            print(f"{name}: {u.get('vgpr')} VGPR + {u.get('agpr')} AGPR, {u.get('vgpr_spill')} spilled VGPRs, "
+                  f"{u.get('scratch')} B scratch per lane, {u.get('sgpr_spill')} spilled SGPRs", file=sys.stderr)
+    bad = check_resources(usage)
+    if bad:
+        raise RuntimeError("register spills above the budget in " + RESOURCE_BUDGET + ":\n  " + "\n  ".join(bad))
     tmp = LIB_PATH + ".tmp"
     cmd = [hipcc, *HIPCC_FLAGS, "-shared", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)

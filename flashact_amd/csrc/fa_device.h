@@ -90,16 +90,26 @@ __device__ __forceinline__ void stb64(rsrc_t r, uint32_t off, u32x2 v) {
 
 // ---------------------------------------------------------------- parity-tagged fp16 exchange
 // Cross-XCD partial sums travel as fp16 whose lowest mantissa bit carries the exchange parity, so
-// data and flag are the same bits (see the batch-1 kernels). Rounding to nearest even and then
-// forcing that bit leaves each value within 2^-10 of its fp32 sum (relative).
+// data and flag are the same bits (see the batch-1 kernels). Rounding to nearest even (<= 0.5 ulp)
+// and then forcing that bit (<= 1 ulp) leaves each value within 1.5 fp16 ulp of its fp32 sum, i.e.
+// within 1.5 * 2^-10 relative for |v| >= 2^-14 and 1.5 * 2^-24 absolute below.
 __device__ __forceinline__ unsigned pack_f16x2(float a, float b) {
   return (unsigned)__builtin_bit_cast(unsigned short, (_Float16)a) |
          ((unsigned)__builtin_bit_cast(unsigned short, (_Float16)b) << 16);
 }
-// Four fp32 values -> four parity-tagged fp16 (8 bytes). `range` collects |v| > 65504.
+// |v| <= 65504 (the largest finite fp16); false for NaN as well.
+__device__ __forceinline__ bool f16_finite(float v) { return fabsf(v) <= 65504.f; }
+// Clamped to the finite fp16 range (NaN becomes 0), so the exchanged bits are never an infinity
+// or a NaN, whose tagged forms would not be values at all.
+__device__ __forceinline__ float f16_clamp(float v) { return f16_finite(v) ? v : (v > 0.f ? 65504.f : (v < 0.f ? -65504.f : 0.f)); }
+// Four fp32 values -> four parity-tagged fp16 (8 bytes). `range` collects values outside the finite
+// fp16 range (or NaN); those are exchanged clamped and the caller raises the sticky range status, so
+// the launch's result is reported invalid instead of carrying an infinity into the residual stream.
 __device__ __forceinline__ u32x2 tag16(f32x4 v, unsigned par, bool& range) {
   const unsigned pp = par * 0x00010001u;
-  range = range || fabsf(v[0]) > 65504.f || fabsf(v[1]) > 65504.f || fabsf(v[2]) > 65504.f || fabsf(v[3]) > 65504.f;
+  const bool ok = f16_finite(v[0]) && f16_finite(v[1]) && f16_finite(v[2]) && f16_finite(v[3]);
+  range = range || !ok;
+  if (!ok) v = f32x4{f16_clamp(v[0]), f16_clamp(v[1]), f16_clamp(v[2]), f16_clamp(v[3])};
   return u32x2{(pack_f16x2(v[0], v[1]) & ~0x00010001u) | pp, (pack_f16x2(v[2], v[3]) & ~0x00010001u) | pp};
 }
 // Non-zero if any of the eight fp16 of v carries the other parity.

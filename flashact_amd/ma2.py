@@ -19,7 +19,7 @@ import ctypes
 
 import torch
 
-from . import _lib
+from . import _lib, pi05
 
 D, NH, HD, FF, AD = 768, 8, 96, 3072, 32
 MAX_TV = 64
@@ -244,5 +244,5 @@ def launch(ws, bs, mods, mod_final, rope_cos, rope_sin, w_ain, b_ain, w_aout, b_
         if st != 0:
             _lib.check(L.fa_ma2_workspace_init(ctypes.c_void_p(wsp.data_ptr()), wsp.numel(),
                                                ctypes.c_void_p(stream.cuda_stream)), "fa_ma2_workspace_init")
-            raise _lib.FlashActError(f"fa_ma2_flow kernel status {st:#x}: the chunk is invalid; the workspace was "
-                                     "re-initialised")
+            raise _lib.FlashActError(f"fa_ma2_flow kernel status {st:#x} ({pi05.describe_status(st)}): the chunk "
+                                     "is invalid; the workspace was re-initialised")

@@ -332,12 +332,28 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
         raise_on_status(ws, stream)
 
 
-def raise_on_status(ws: torch.Tensor, stream=None) -> None:
+# Kernel status bits (FA_KSTATUS_* of include/flashact_mi355x.h).
+STATUS_BITS = {
+    1: "1 = a capped barrier wait expired",
+    2: "2 = the workgroup -> XCD placement differed from round robin",
+    4: "4 = an exchanged partial sum left the finite fp16 range and was clamped",
+}
+
+
+def describe_status(st: int) -> str:
+    parts = [text for bit, text in STATUS_BITS.items() if st & bit]
+    rest = st & ~sum(STATUS_BITS)
+    if rest:
+        parts.append(f"unknown bits {rest:#x}")
+    return "; ".join(parts) or "ok"
+
+
+def raise_on_status(ws: torch.Tensor, stream=None, what: str = "fa_pi05_denoise") -> None:
     """Waits for `stream`, reads the kernel status of the workspace's last launch; a non-zero status
     re-initialises the workspace (its control words are then undefined) and raises FlashActError."""
     (stream or torch.cuda.current_stream(ws.device)).synchronize()
     st = read_status(ws)
     if st != 0:
         reset_workspace(ws)
-        raise _lib.FlashActError(f"fa_pi05_denoise kernel status {st:#x} (1 = capped wait expired, 2 = XCD placement "
-                                 "differed): the chunk is invalid; the workspace was re-initialised")
+        raise _lib.FlashActError(f"{what} kernel status {st:#x} ({describe_status(st)}): the result is invalid; "
+                                 "the workspace was re-initialised")

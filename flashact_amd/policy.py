@@ -167,8 +167,10 @@ class Pi05Policy:
         srows = 0
         if prefix_hidden is not None:
             b = self.backbone
+            # check_status: a prefill whose barriers expired leaves the caches unfinished; it raises
+            # here (after re-initialising its workspace) before the denoise loop reads them
             prefill.prefill(b["packed"], b["ln_in"], b["ln_post"], prefix_hidden.to(dev, torch.float32).contiguous(),
-                            kc, vc)
+                            kc, vc, check_status=True)
         else:
             ksrc, vsrc = kv_rows[0].contiguous(), kv_rows[1].contiguous()
             srows = int(ksrc.shape[-2])
@@ -178,7 +180,8 @@ class Pi05Policy:
         empty = torch.empty(0, device=dev)
         sc = [p.get(k, empty) for k in ("s1", "so", "s2", "s3")]
         # check_status: waits for the chunk and raises (after re-initialising the workspace) if a
-        # capped wait expired or the XCD placement differed, so an invalid chunk is never returned
+        # capped wait expired, the XCD placement differed or an exchanged partial sum left the fp16
+        # range, so an invalid chunk is never returned
         pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], *sc, self.mods, self.mod_final,
                     cos, sin, self.w_ain, self.b_ain, self.w_aout, self.b_aout, ksrc, vsrc, srows, kc, vc, Lp, Lmax,
                     self.num_steps, self.chunk_size, x_t, check_status=True)

@@ -75,8 +75,12 @@ def _ptr(t, name):
 
 
 def prefill(packed: dict, ln_in, ln_post, x, kcache, vtcache, rope_cos=None, rope_sin=None, *, stage_cycles=None,
-            workspace_tensor=None):
+            workspace_tensor=None, check_status=False):
     """Runs every backbone layer over the prefix and fills the caches in place.
+
+    check_status=True waits for the launch and reads the kernel status; a non-zero status (a capped
+    barrier wait expired, or the XCD placement differed, which leaves the caches unfinished)
+    re-initialises the workspace and raises FlashActError.
 
     packed: ``pack_backbone`` output. ln_in, ln_post [NL][2048] fp32. x [B][Lp][2048] (or [Lp][2048])
     fp32: the hidden states entering layer 0. kcache [B][NL][Lmax][256] / vtcache [B][NL][256][Lmax]
@@ -119,3 +123,5 @@ def prefill(packed: dict, ln_in, ln_post, x, kcache, vtcache, rope_cos=None, rop
     a.workspace, a.workspace_bytes = wsp.data_ptr(), wsp.numel()
     stream = torch.cuda.current_stream(dev).cuda_stream
     _lib.check(L.fa_pi05_prefill(ctypes.byref(a), ctypes.c_void_p(stream)), "fa_pi05_prefill")
+    if check_status:
+        pi05.raise_on_status(wsp, torch.cuda.current_stream(dev), what="fa_pi05_prefill")

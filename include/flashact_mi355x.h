@@ -54,8 +54,9 @@ enum fa_dtype { FA_DTYPE_BF16 = 0, FA_DTYPE_FP8_E4M3 = 1, FA_DTYPE_F16 = 2 };
 /* Kernel-side status bits (read back from the workspace by fa_*_read_status). */
 #define FA_KSTATUS_SPIN_TIMEOUT 1u /* a grid/XCD barrier wait hit its cap: results invalid */
 #define FA_KSTATUS_XCD_MAP 2u      /* workgroup -> XCD placement differed from round robin */
-#define FA_KSTATUS_RANGE 4u        /* a partial sum exchanged between XCDs exceeded the fp16 range
-                                    * (|v| > 65504) in a batch-1 kernel: results invalid */
+#define FA_KSTATUS_RANGE 4u        /* a partial sum exchanged between XCDs left the finite fp16
+                                    * range (|v| > 65504, or NaN) in the pi0.5 batch-1 kernel; it was
+                                    * exchanged clamped to +-65504: results invalid */
 
 typedef struct fa_device_info {
   int cus;               /* compute units */

@@ -50,6 +50,21 @@ static inline float bf(uint16_t h) {
   return f;
 }
 
+/* IEEE 754 binary16 -> fp32 (exact): sign, 5-bit exponent (bias 15), 10-bit fraction; exponent 0
+ * holds the subnormals frac * 2^-24, exponent 31 the infinities and NaNs. */
+static inline float h2f(uint16_t h) {
+  const int sgn = h >> 15, ex = (h >> 10) & 31, fr = h & 1023;
+  float v;
+  if (ex == 0) v = ldexpf((float)fr, -24);
+  else if (ex == 31) v = fr ? NAN : INFINITY;
+  else v = ldexpf((float)(1024 + fr), ex - 25);
+  return sgn ? -v : v;
+}
+
+void fo_f16_decode(const uint16_t* bits, int n, float* out) {
+  for (int i = 0; i < n; i++) out[i] = h2f(bits[i]);
+}
+
 static inline float dot_f32(const float* a, const float* b, int n) {
   /* 8 independent partial sums so the compiler can vectorise without -ffast-math */
   float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -263,6 +278,7 @@ void fo_rope_table(int start, int T, int HD, double base, float* cosv, float* si
 typedef struct {
   int NL, D, H, HD, F, AD;
   int Lp, Tv, S, batch;
+  int kv_f16; /* 0: kpre / vpre hold bf16 bits; 1: fp16 bits (the reference's cache dtype) */
 } fo_pi05_dims;
 
 /* Weights (bf16 bits, natural layouts):
@@ -271,7 +287,7 @@ typedef struct {
  * mods [S][NL][2][3D] (scale|shift|gate), mod_final [S][3D]
  * rope_cos/sin [Tv][HD/2] for positions Lp + t
  * w_ain [D][AD], b_ain [D], w_aout [AD][D], b_aout [AD] (fp32)
- * kpre, vpre [batch][NL][Lp][HD] bf16 (already-RoPE'd prefix keys, values)
+ * kpre, vpre [batch][NL][Lp][HD] bf16, or fp16 with kv_f16 (already-RoPE'd prefix keys, values)
  * x_t [batch][Tv][AD] fp32, updated in place. */
 static int pi05_loop(const fo_pi05_dims* dm, fo_wmat wq, fo_wmat wk, fo_wmat wv, fo_wmat wo, fo_wmat wg, fo_wmat wu,
                      fo_wmat wd, const float* mods, const float* mod_final, const float* rope_cos,
@@ -324,7 +340,10 @@ static int pi05_loop(const fo_pi05_dims* dm, fo_wmat wq, fo_wmat wk, fo_wmat wv,
         }
         const uint16_t* kp = kpre + (((size_t)b * NL + l) * Lp) * HD;
         const uint16_t* vp = vpre + (((size_t)b * NL + l) * Lp) * HD;
-        for (size_t i = 0; i < (size_t)Lp * HD; i++) { Kl[i] = bf(kp[i]); Vl[i] = bf(vp[i]); }
+        if (dm->kv_f16)
+          for (size_t i = 0; i < (size_t)Lp * HD; i++) { Kl[i] = h2f(kp[i]); Vl[i] = h2f(vp[i]); }
+        else
+          for (size_t i = 0; i < (size_t)Lp * HD; i++) { Kl[i] = bf(kp[i]); Vl[i] = bf(vp[i]); }
         memcpy(Kl + (size_t)Lp * HD, k, sizeof(float) * (size_t)Tv * HD);
         memcpy(Vl + (size_t)Lp * HD, v, sizeof(float) * (size_t)Tv * HD);
 #pragma omp parallel

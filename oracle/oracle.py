@@ -28,7 +28,7 @@ def build(force: bool = False) -> str:
 
 
 class Pi05Dims(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_int) for n in ("NL", "D", "H", "HD", "F", "AD", "Lp", "Tv", "S", "batch")]
+    _fields_ = [(n, ctypes.c_int) for n in ("NL", "D", "H", "HD", "F", "AD", "Lp", "Tv", "S", "batch", "kv_f16")]
 
 
 class PrefillDims(ctypes.Structure):
@@ -73,6 +73,12 @@ def _u16(a):
     return a
 
 
+def _kv_f16(kv_dtype: str) -> int:
+    if kv_dtype not in ("bf16", "f16"):
+        raise ValueError(f"kv_dtype must be 'bf16' or 'f16', got {kv_dtype!r}")
+    return int(kv_dtype == "f16")
+
+
 def num_threads() -> int:
     return int(lib().fo_num_threads())
 
@@ -104,15 +110,16 @@ def pi05_mods(S: int, NL: int, D: int, w_ti, b_ti, w_to, b_to, w_in, b_in, w_pos
 
 
 def pi05_denoise(w: dict, x_t, *, Lp: int, Tv: int, S: int, NL: int, D: int = 1024, H: int = 8, HD: int = 256,
-                 F: int = 4096, AD: int = 32) -> np.ndarray:
+                 F: int = 4096, AD: int = 32, kv_dtype: str = "bf16") -> np.ndarray:
     """Runs the S-step Euler loop; returns the updated x_t [batch][Tv][AD].
 
     ``w`` keys: wq wk wv wo wg wu wd (uint16 bf16 bits, natural layouts), mods, mod_final,
-    rope_cos, rope_sin, w_ain, b_ain, w_aout, b_aout (fp32), kpre, vpre ([B][NL][Lp][HD] bf16 bits).
+    rope_cos, rope_sin, w_ain, b_ain, w_aout, b_aout (fp32), kpre, vpre ([B][NL][Lp][HD] bf16 bits,
+    or fp16 bits with kv_dtype="f16").
     """
     x = _f32(x_t).copy()
     B = x.shape[0] if x.ndim == 3 else 1
-    dims = Pi05Dims(NL, D, H, HD, F, AD, Lp, Tv, S, B)
+    dims = Pi05Dims(NL, D, H, HD, F, AD, Lp, Tv, S, B, _kv_f16(kv_dtype))
     u = {k: _u16(w[k]) for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd", "kpre", "vpre")}
     f = {k: _f32(w[k]) for k in ("mods", "mod_final", "rope_cos", "rope_sin", "w_ain", "b_ain", "w_aout", "b_aout")}
     rc = lib().fo_pi05_denoise(
@@ -125,6 +132,14 @@ def pi05_denoise(w: dict, x_t, *, Lp: int, Tv: int, S: int, NL: int, D: int = 10
     return x
 
 
+def f16_decode(bits) -> np.ndarray:
+    """fp32 values of IEEE binary16 bit patterns (uint16)."""
+    c = _u16(bits)
+    out = np.empty(c.shape, np.float32)
+    lib().fo_f16_decode(_p(c, np.uint16), ctypes.c_int(c.size), _p(out, np.float32))
+    return out
+
+
 def e4m3_decode(codes) -> np.ndarray:
     """fp32 values of OCP E4M3 codes (uint8)."""
     c = np.ascontiguousarray(codes, dtype=np.uint8)
@@ -134,13 +149,13 @@ def e4m3_decode(codes) -> np.ndarray:
 
 
 def pi05_denoise_fp8(w: dict, x_t, *, Lp: int, Tv: int, S: int, NL: int, D: int = 1024, H: int = 8, HD: int = 256,
-                     F: int = 4096, AD: int = 32) -> np.ndarray:
+                     F: int = 4096, AD: int = 32, kv_dtype: str = "bf16") -> np.ndarray:
     """pi05_denoise with FP8-W8A16 weights: ``w`` holds e4m3 codes qq qk qv qo qg qu qd (uint8,
-    natural layouts) and their per-row fp32 scales sq sk sv so sg su sd, plus the fp32 / bf16 inputs
-    of ``pi05_denoise``."""
+    natural layouts) and their per-row fp32 scales sq sk sv so sg su sd, plus the fp32 / bf16 (or
+    fp16 K/V) inputs of ``pi05_denoise``."""
     x = _f32(x_t).copy()
     B = x.shape[0] if x.ndim == 3 else 1
-    dims = Pi05Dims(NL, D, H, HD, F, AD, Lp, Tv, S, B)
+    dims = Pi05Dims(NL, D, H, HD, F, AD, Lp, Tv, S, B, _kv_f16(kv_dtype))
     q = {k: np.ascontiguousarray(w[k], dtype=np.uint8) for k in ("qq", "qk", "qv", "qo", "qg", "qu", "qd")}
     sc = {k: _f32(w[k]) for k in ("sq", "sk", "sv", "so", "sg", "su", "sd")}
     f = {k: _f32(w[k]) for k in ("mods", "mod_final", "rope_cos", "rope_sin", "w_ain", "b_ain", "w_aout", "b_aout")}

@@ -58,11 +58,14 @@ def kv_diff(kc, vt, K, V, Lp):
 
 
 def run_bf16_floor(c):
-    """(K, V) [batch][NL][Lp][256] of a torch restatement of the prefill in fp32 arithmetic whose
-    matmul operands are rounded to bf16 where bf16 MFMAs take them: the normed rows, q, k, v, the
-    softmax weights of each 128-key chunk and that chunk's normalised output, the combined attention
-    output and the MLP activation. Its distance to the fp32 oracle is the error that bf16 operands
-    alone produce (the floor a bf16 kernel is held to); it is not the oracle."""
+    """(K, V) [batch][NL][Lp][256] of a torch restatement of the prefill in fp32 arithmetic that
+    rounds to bf16 exactly where the kernel does: the matmul operands bf16 MFMAs take (the normed rows,
+    q, k, v, the softmax weights of each 128-key chunk and that chunk's normalised output, the
+    combined attention output, the MLP activation) and the K-split partial sums the kernel stores in
+    bf16 (the O projection in 2 K ranges of 1024, the down projection in 8 of 2048, each partial
+    rounded once before the next norm adds them to the fp32 residual). Its distance to the fp32
+    oracle is the error those roundings alone produce (the floor a bf16 kernel is held to); it is
+    not the oracle."""
     w = c["w"]
     bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
     cos, sin = c["cos"].float(), c["sin"].float()
@@ -103,11 +106,14 @@ def run_bf16_floor(c):
             wsum = sum(l_ * torch.exp(m_ - M) for l_, m_ in zip(ls, ms))
             att = sum(o * l_ * torch.exp(m_ - M) for o, l_, m_ in zip(outs, ls, ms)) / wsum
             att = bf(att).permute(1, 0, 2).reshape(Lp, 8 * 256)
-            x = x + att @ w["wo"][l].float().cpu().T
+            wo = w["wo"][l].float().cpu()
+            x = x + sum(bf(att[:, k0:k0 + 1024] @ wo[:, k0:k0 + 1024].T) for k0 in range(0, 2048, 1024))
             h = bf(rms(x, w["ln_post"][l].float().cpu()))
             g = h @ w["wg"][l].float().cpu().T
             u = h @ w["wu"][l].float().cpu().T
-            x = x + bf(torch.nn.functional.gelu(g, approximate="tanh") * u) @ w["wd"][l].float().cpu().T
+            m = bf(torch.nn.functional.gelu(g, approximate="tanh") * u)
+            wd = w["wd"][l].float().cpu()
+            x = x + sum(bf(m[:, k0:k0 + 2048] @ wd[:, k0:k0 + 2048].T) for k0 in range(0, 16384, 2048))
         Ks.append(torch.stack(kl))
         Vs.append(torch.stack(vl))
     return torch.stack(Ks).numpy(), torch.stack(Vs).numpy()

@@ -194,3 +194,23 @@ def test_prefill_without_device(lib):
     assert lib.fa_pi05_prefill_workspace_bytes(4, 968, 1024) > one
     assert lib.fa_pi05_prefill_workspace_bytes(1, 968, 960) == 0
     assert lib.fa_pi05_prefill_workspace_bytes(17, 968, 1024) == 0
+
+
+def test_resource_report_parses_and_budget_holds():
+    """build.py reads each kernel's register use from the compiler's remarks and refuses spills above
+    flashact_amd/resource_budget.json; the report of the library built here is within it."""
+    import json
+    from flashact_amd import build
+    text = ("x.hip:1:1: remark: Function Name: _Zk [-Rpass-analysis=kernel-resource-usage]\n"
+            "x.hip:1:1: remark:     VGPRs: 256 [-Rpass-analysis=kernel-resource-usage]\n"
+            "x.hip:1:1: remark:     AGPRs: 12 [-Rpass-analysis=kernel-resource-usage]\n"
+            "x.hip:1:1: remark:     ScratchSize [bytes/lane]: 8 [-Rpass-analysis=kernel-resource-usage]\n"
+            "x.hip:1:1: remark:     SGPRs Spill: 3 [-Rpass-analysis=kernel-resource-usage]\n"
+            "x.hip:1:1: remark:     VGPRs Spill: 2 [-Rpass-analysis=kernel-resource-usage]\n")
+    u = build.parse_resource_usage(text)
+    assert u == {"_Zk": {"vgpr": 256, "agpr": 12, "scratch": 8, "sgpr_spill": 3, "vgpr_spill": 2}}
+    assert build.check_resources(u)  # an unlisted kernel may not spill
+    if os.path.exists(build.RESOURCE_REPORT):
+        rep = json.load(open(build.RESOURCE_REPORT))
+        assert any("pi05_denoise_bs1" in k for k in rep)
+        assert build.check_resources(rep) == []

@@ -1,0 +1,61 @@
+"""The batch-1 pi0.5 kernel's cross-XCD exchange: the O and down partial sums (one per XCD K-window)
+travel as fp16 with the exchange parity in the lowest mantissa bit; the reference keeps them in fp32
+(src/pi05/mk6.cu:63 ``float* xp``, summed at mk6.cu:147).
+
+* A partial outside the finite fp16 range is exchanged clamped to +-65504 and raises the sticky
+  FA_KSTATUS_RANGE bit: the output stays finite, ``launch(check_status=True)`` raises and
+  re-initialises the workspace, and the next launch runs clean. The inputs are built on the host so
+  that every XCD's O partial of output column 0 is about 400 * 256 * 0.95 = 97,000: W_o row 0 is 400
+  everywhere, the prefix values are all 1 and W_v is zero, so each head's attention output is the
+  softmax weight of the prefix keys (about 0.95) in every dim. No wait, index or loop bound depends on
+  the values, so the launch runs exactly as on ordinary inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from flashact_amd import _lib, pi05
+from tests import pi05_case as P
+
+pytestmark = pytest.mark.gpu
+
+
+def _range_case():
+    c = P.make_case(NL=2, Lp=968, Tv=50, S=2, seed=31)
+    w = c["w"]
+    w["wo"][0, 0, :] = 400.0  # bf16-exact
+    w["wv"][:] = 0.0
+    c["inp"]["vpre"][:] = 1.0
+    return c
+
+
+def test_exchange_range_sets_status_and_stays_finite(gpu):
+    c = _range_case()
+    g = P.gpu_tensors(c, gpu)
+    ws = pi05.workspace(gpu)
+    pi05.reset_workspace(ws)
+    out = P.run_gpu(c, gpu, g)[0]
+    st = pi05.read_status(ws)
+    print(f"range case: status {st:#x}, max |x_t| {np.abs(out).max():.3g}", flush=True)
+    assert st & _lib.FA_KSTATUS_RANGE, f"status {st:#x}: the O partial of column 0 is ~1e5 > 65504"
+    assert st & ~_lib.FA_KSTATUS_RANGE == 0
+    assert np.isfinite(out).all(), "clamped partials must never carry inf / NaN into x_t"
+
+    # the drop-in call with check_status raises and re-initialises the workspace ...
+    pk = g["packed"]
+    kc, vc = g["caches"][0]
+    e = torch.empty(0, device=gpu)
+    x_t = c["inp"]["noise"][0].to(gpu).clone()
+    with pytest.raises(_lib.FlashActError, match="fp16 range"):
+        pi05.launch(pk["w1"], pk["wo"], pk["w2"], pk["w3"], e, e, e, e, g["mods"], g["mod_final"], g["cos"],
+                    g["sin"], g["w_ain"], g["b_ain"], g["w_aout"], g["b_aout"], None, None, 0, kc, vc, c["Lp"],
+                    g["Lmax"], c["S"], c["Tv"], x_t, check_status=True)
+    assert pi05.read_status(ws) == 0
+
+    # ... and an ordinary case on the same workspace afterwards is clean and within tolerance
+    c2 = P.make_case(NL=2, Lp=968, Tv=50, S=2, seed=32)
+    ref = P.run_oracle(c2)[0]
+    out2 = P.run_gpu(c2, gpu)[0]
+    st2 = P.parity(out2[:50], ref)
+    assert pi05.read_status(ws) == 0
+    assert st2["max_abs"] <= 2e-2 and st2["mean_abs"] <= 2e-3, st2

@@ -67,20 +67,23 @@ def config3(gpu):
 def test_prefill_config3_all_layers(config3):
     """The full BASELINE config 3 launch: K/V of every one of the 18 layers against the oracle.
 
-    Through 18 layers of a 2048-wide residual stream the bf16 operand roundings compound: the error
-    to the fp32 oracle grows from 1.7e-3 (layer 0) to about 7.6e-3 mean-abs (layer 17) for K and V
-    of unit scale. Each layer is therefore held to the error of a bf16-operand restatement
-    (prefill_case.run_bf16_floor) on the same inputs: mean-abs within 1.15x that floor + 2e-4 and
-    max-abs within 1.5x + 5e-3; layers 0-1 also to the fixed gates (4e-2 max, 4e-3 mean)."""
+    Through 18 layers of a 2048-wide residual stream the bf16 roundings compound: the error to the
+    fp32 oracle grows from 1.7e-3 (layer 0) to about 8.7e-3 mean-abs (layer 17) for K and V of unit
+    scale. Each layer is therefore held to the error of a restatement that rounds exactly where the
+    kernel rounds (bf16 operands and bf16 K-split partials, prefill_case.run_bf16_floor) on the same
+    inputs: mean-abs within 1.05x that floor + 1e-4 and max-abs within 1.5x + 5e-3; layers 0-1 also to
+    the fixed gates (4e-2 max, 4e-3 mean). The mean-abs ratio to the floor is printed per layer."""
     c, kc, vt, K, V, _ = config3
     Kf, Vf = C.run_bf16_floor(c)
     for l in range(c["NL"]):
         st = C.kv_diff(kc[:, l:l + 1], vt[:, l:l + 1], K[:, l:l + 1], V[:, l:l + 1], c["Lp"])
         fk, fv = np.abs(Kf[:, l] - K[:, l]), np.abs(Vf[:, l] - V[:, l])
         fl = {"k_mean": float(fk.mean()), "k_max": float(fk.max()), "v_mean": float(fv.mean()), "v_max": float(fv.max())}
-        print(f"config 3 prefill layer {l}: {st}; bf16 floor {fl}", flush=True)
+        ratio = {kv: st[f"{kv}_mean"] / max(fl[f"{kv}_mean"], 1e-30) for kv in ("k", "v")}
+        print(f"config 3 prefill layer {l}: {st}; bf16 floor {fl}; mean-abs / floor K {ratio['k']:.3f} "
+              f"V {ratio['v']:.3f}", flush=True)
         for kv in ("k", "v"):
-            assert st[f"{kv}_mean"] <= 1.15 * fl[f"{kv}_mean"] + 2e-4, (l, kv, st, fl)
+            assert st[f"{kv}_mean"] <= 1.05 * fl[f"{kv}_mean"] + 1e-4, (l, kv, st, fl)
             assert st[f"{kv}_max"] <= 1.5 * fl[f"{kv}_max"] + 5e-3, (l, kv, st, fl)
         if l < 2:
             assert st["k_max"] <= KV_MAX and st["v_max"] <= KV_MAX, (l, st)

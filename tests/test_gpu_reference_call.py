@@ -5,9 +5,10 @@ fp16 caches kcache [NL][Lmax][256] / vtcache [NL][256][Lmax] with Lmax = ceil16(
 T = 16 rows of which Tv = 10 are valid, the fp32 / fp16 scratch tensors x, xp, xn, q, attn, hmlp,
 scores, probs, an int64 stage counter, empty bf16 hand-off tensors with srows = 0, and 170 x 256
 threads; then calls ``launch`` with them in that order. The same call here must match the
-oracle's fp8 loop on the same codes, scales and cache values (fp16 cache values reach the bf16
-MFMAs rounded to bf16, which the oracle is given), write the suffix rows back into the fp16
-caches, and leave rows [Tv, T) of x_t alone.
+oracle's fp8 loop on the same codes, scales and the caller's fp16 cache values as they are (the
+oracle reads the fp16 bits; nothing is rounded for it), write the suffix rows back into the fp16
+caches, and leave rows [Tv, T) of x_t alone. Each launch starts from a freshly initialised
+workspace, so a comparison of two launches does not depend on the workspace's exchange history.
 """
 import numpy as np
 import pytest
@@ -43,7 +44,7 @@ def test_reference_call_fp8_fp16_caches(gpu):
     c = P.make_case(NL=NL, Lp=Lp, Tv=TV, S=S, seed=21)
     Lmax = (Lp + T + 15) // 16 * 16
     kh, vh = _fp16_caches(NL, Lp, Lmax, seed=22)
-    c["inp"]["kpre"], c["inp"]["vpre"] = kh.bfloat16(), vh.bfloat16()
+    c["inp"]["kpre"], c["inp"]["vpre"] = kh.bfloat16(), vh.bfloat16()  # the GPU side reads kh / vh below
     w = c["w"]
     nat = {k: w[k] for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")}
     pk = pi05.pack_weights_fp8(*(nat[k].to(gpu) for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")))
@@ -65,6 +66,7 @@ def test_reference_call_fp8_fp16_caches(gpu):
     mods, modf = c["mods"].to(dev), c["mod_final"].to(dev)
     wv = {k: w[k].to(dev) for k in ("w_ain", "b_ain", "w_aout", "b_aout")}
     empty = torch.empty(0, dtype=torch.bfloat16, device=dev)
+    pi05.reset_workspace(pi05.workspace(dev))
     pi05.launch(pk["w1"], pk["wo"], pk["w2"], pk["w3"], pk["s1"], pk["so"], pk["s2"], pk["s3"],
                 mods, modf, cos, sin, wv["w_ain"], wv["b_ain"], wv["w_aout"], wv["b_aout"],
                 empty, empty, 0, kcache, vtcache, Lp, Lmax, S, TV, x_t, x, xp, sc_cyc,
@@ -78,9 +80,12 @@ def test_reference_call_fp8_fp16_caches(gpu):
     for n, k in (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo"), ("g", "wg"), ("u", "wu"), ("d", "wd")):
         q, s = pi05.quantize_fp8(nat[k])
         ow["q" + n], ow["s" + n] = q.numpy(), s.numpy()
-    ref = O.pi05_denoise_fp8(ow, c["inp"]["noise"].numpy(), Lp=Lp, Tv=TV, S=S, NL=NL)[0]
+    ow["kpre"] = kh.numpy().view(np.uint16)  # the caller's fp16 values, unrounded
+    ow["vpre"] = vh.numpy().view(np.uint16)
+    ref = O.pi05_denoise_fp8(ow, c["inp"]["noise"].numpy(), Lp=Lp, Tv=TV, S=S, NL=NL, kv_dtype="f16")[0]
     st = P.parity(out[:TV], ref)
-    print(f"reference call (fp8 codes, fp16 caches, T=16, Tv=10, 18 layers x 10 steps): {st}", flush=True)
+    print(f"reference call (fp8 codes, fp16 caches, T=16, Tv=10, 18 layers x 10 steps) vs the oracle on the "
+          f"fp16 cache values: {st}", flush=True)
     assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
     assert np.all(out[TV:] == 0.0), "rows [Tv, T) of x_t must be left untouched"
     assert int(sc_cyc.sum()) > 0
@@ -91,6 +96,7 @@ def test_reference_call_fp8_fp16_caches(gpu):
     kb, vb = kb[0].contiguous(), vb[0].contiguous()
     x2 = torch.zeros(T, AD, dtype=torch.float32, device=dev)
     x2[:TV] = c["inp"]["noise"][0].to(dev)
+    pi05.reset_workspace(pi05.workspace(dev))
     pi05.launch(pk["w1"], pk["wo"], pk["w2"], pk["w3"], pk["s1"], pk["so"], pk["s2"], pk["s3"],
                 mods, modf, cos, sin, wv["w_ain"], wv["b_ain"], wv["w_aout"], wv["b_aout"],
                 empty, empty, 0, kb, vb, Lp, Lmax, S, TV, x2)

@@ -148,6 +148,44 @@ def test_predict_checks_the_kernel_status(monkeypatch):
     assert seen.get("check_status") is True and out.shape == (10, 32)
 
 
+def test_predict_checks_the_prefill_status(monkeypatch):
+    """A prefill whose status is non-zero leaves the caches unfinished: predict asks prefill to check
+    its status, and a raise there stops the chunk before the denoise loop reads the caches."""
+    from flashact_amd import prefill
+    seen = {}
+    pol = policy.Pi05Policy(PC.checkpoint(NL=2, seed=1), device="cpu", load_backbone=False, chunk_size=10)
+    pol.backbone = {"packed": None, "ln_in": None, "ln_post": None}
+    monkeypatch.setattr(prefill, "prefill", lambda *a, **kw: seen.setdefault("prefill", kw))
+    monkeypatch.setattr(pi05, "launch", lambda *a, **kw: seen.setdefault("launch", kw))
+    pol.predict(prefix_hidden=torch.zeros(16, 2048))
+    assert seen["prefill"].get("check_status") is True and seen["launch"].get("check_status") is True
+
+    def bad_prefill(*a, **kw):
+        raise _lib.FlashActError("fa_pi05_prefill kernel status 0x1")
+    seen.clear()
+    monkeypatch.setattr(prefill, "prefill", bad_prefill)
+    with pytest.raises(_lib.FlashActError, match="prefill"):
+        pol.predict(prefix_hidden=torch.zeros(16, 2048))
+    assert "launch" not in seen
+
+
+@pytest.mark.parametrize("st,text", [(1, "capped barrier wait"), (2, "XCD"), (4, "fp16 range"),
+                                     (5, "capped barrier wait expired; 4 = an exchanged"), (8, "unknown bits 0x8")])
+def test_status_message_names_every_bit(monkeypatch, st, text):
+    monkeypatch.setattr(pi05, "read_status", lambda ws: st)
+    monkeypatch.setattr(pi05, "reset_workspace", lambda ws: None)
+    with pytest.raises(_lib.FlashActError, match=text):
+        pi05.raise_on_status(torch.zeros(4), _Stream())
+
+
+def test_status_bits_match_the_header():
+    import os
+    import re
+    hdr = open(os.path.join(os.path.dirname(__file__), "..", "include", "flashact_mi355x.h")).read()
+    bits = {int(v.rstrip("u")) for v in re.findall(r"#define FA_KSTATUS_\w+ (\d+u)", hdr)}
+    assert bits == set(pi05.STATUS_BITS)
+
+
 def _c_args(**kw):
     a = _lib.Pi05Args()
     fake = 1 << 20

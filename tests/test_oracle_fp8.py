@@ -6,6 +6,9 @@
   loops must agree bit for bit (a scale applied twice, to the wrong row, or not at all breaks it).
 * quantize_fp8 (the reference's per-row quantisation, src/pi05/hybrid_model.py:105-110): the
   largest element of each row maps to +-448 and the round trip stays within e4m3's step.
+* fp16 prefix K/V (the reference's cache dtype, benchmarks/pi05/eval_numerics.py:83-85): the
+  oracle's binary16 decoding against numpy's float16 on all 65536 bit patterns, and the loop on fp16
+  bits equal, bit for bit, to the loop on bf16 bits when every value is exact in both formats.
 """
 import numpy as np
 import torch
@@ -24,6 +27,16 @@ def test_e4m3_decode_all_codes():
     ok = ~np.isnan(want)
     assert np.array_equal(got[ok], want[ok])
     assert np.array_equal(np.signbit(got[ok]), np.signbit(want[ok]))  # -0 is 0x80
+
+
+def test_f16_decode_all_patterns():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.f16_decode(bits)
+    want = bits.view(np.float16).astype(np.float32)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok], want[ok])
+    assert np.array_equal(np.signbit(got[ok]), np.signbit(want[ok]))
 
 
 def _case(rng, Lp=5, Tv=3, S=2):
@@ -64,6 +77,27 @@ def test_fp8_loop_equals_bf16_loop_on_dequantised_weights():
     w2 = dict(w)
     w2["sg"] = w["sg"] * 2
     assert not np.array_equal(O.pi05_denoise_fp8(w2, x, Lp=Lp, Tv=Tv, S=S, **DIMS), out8)
+
+
+def test_f16_kv_loop_equals_bf16_kv_loop_on_shared_values():
+    rng = np.random.default_rng(3)
+    w, x, Lp, Tv, S = _case(rng)
+    wb = dict(w)
+    for n in "qkvogud":
+        deq = O.e4m3_decode(w["q" + n]) * w["s" + n][..., None]
+        wb["w" + n] = torch.from_numpy(deq).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    wh = dict(wb)
+    for k in ("kpre", "vpre"):
+        vals = (w[k].astype(np.uint32) << 16).view(np.float32)
+        vals = np.where(np.abs(vals) < 2.0 ** -14, 0.0, vals).astype(np.float32)  # normal in fp16 too
+        wb[k] = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        wh[k] = vals.astype(np.float16).view(np.uint16)
+        assert np.array_equal(wh[k].view(np.float16).astype(np.float32), vals)  # exact in fp16
+    ob = O.pi05_denoise(wb, x, Lp=Lp, Tv=Tv, S=S, **DIMS)
+    oh = O.pi05_denoise(wh, x, Lp=Lp, Tv=Tv, S=S, kv_dtype="f16", **DIMS)
+    assert np.array_equal(ob, oh)
+    # the same bits read as the other format are other values
+    assert not np.array_equal(O.pi05_denoise(wb, x, Lp=Lp, Tv=Tv, S=S, kv_dtype="f16", **DIMS), ob)
 
 
 def test_quantize_fp8_rows():

@@ -16,6 +16,9 @@ LIB_PATH = os.path.join(LIB_DIR, "libflashact_mi355x.so")
 # C++ host program that calls the C ABI directly (tests/cabi_driver.cpp), run by the GPU tests
 DRIVER_SRC = os.path.join(ROOT, "tests", "cabi_driver.cpp")
 DRIVER_PATH = os.path.join(ROOT, "tests", "bin", "cabi_driver")
+# litmus tests of the cross-CU / cross-XCD message passing the kernels rely on (tests/litmus_xcd.hip)
+LITMUS_SRC = os.path.join(ROOT, "tests", "litmus_xcd.hip")
+LITMUS_PATH = os.path.join(ROOT, "tests", "bin", "litmus_xcd")
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -121,6 +124,7 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc link failed ({res.returncode}):\n{out}")
     os.replace(tmp, LIB_PATH)
     build_driver(hipcc)
+    build_litmus(hipcc)
     return LIB_PATH
 
 
@@ -137,6 +141,17 @@ def build_driver(hipcc: str) -> str:
         raise RuntimeError(f"hipcc failed on {DRIVER_SRC} ({res.returncode}):\n{res.stdout}{res.stderr}")
     os.replace(tmp, DRIVER_PATH)
     return DRIVER_PATH
+
+
+def build_litmus(hipcc: str) -> str:
+    os.makedirs(os.path.dirname(LITMUS_PATH), exist_ok=True)
+    tmp = LITMUS_PATH + ".tmp"
+    cmd = [hipcc, *HIPCC_FLAGS, LITMUS_SRC, "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {LITMUS_SRC} ({res.returncode}):\n{res.stdout}{res.stderr}")
+    os.replace(tmp, LITMUS_PATH)
+    return LITMUS_PATH
 
 
 if __name__ == "__main__":

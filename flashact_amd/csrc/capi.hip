@@ -68,6 +68,20 @@ int check_device(const void* kernel, int threads, unsigned lds_bytes, int nwg, c
   return FA_OK;
 }
 
+int coop_launch(const void* kernel, int nwg, int threads, void** args, unsigned lds, fa_stream_t stream,
+                const char* who) {
+  const hipError_t e =
+      hipLaunchCooperativeKernel(kernel, dim3(nwg), dim3(threads), args, lds, (hipStream_t)stream);
+  if (e == hipSuccess) return FA_OK;
+  if (e == hipErrorIllegalState)
+    return fail(FA_ERR_LAUNCH,
+                "%s: the runtime refused the cooperative launch (%s). This happens in a process whose parent "
+                "had already made a cooperative launch when it started this one: start worker processes before "
+                "the parent's first launch (or from a parent that never launches)",
+                who, hipGetErrorString(e));
+  return fail(FA_ERR_LAUNCH, "%s: cooperative launch failed: %s", who, hipGetErrorString(e));
+}
+
 }  // namespace host
 }  // namespace fa
 

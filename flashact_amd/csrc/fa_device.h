@@ -131,6 +131,14 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                  0, 0);
 }
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+// The same product with fp16 operands (v_mfma_f32_16x16x32_f16, the bf16 rate on gfx950): the
+// batch-1 attention on the caller's fp16 caches.
+__device__ __forceinline__ f32x4 mfma16h(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
+}
+
 // hipcc (ROCm 7.2, clang 22) evaluates __builtin_bit_cast(T, v[i]) on an element of an
 // ext_vector_type as a cast of element 0. Element reinterpretation therefore goes through
 // these value-parameter helpers; flashact_amd/build.py rejects the direct form in csrc/.

@@ -20,6 +20,13 @@ inline int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+// Enqueues the cooperative launch of `kernel` (nwg x threads, `lds` bytes of dynamic LDS). On failure
+// the error text names the runtime's reason; hipErrorIllegalState is the refusal a process gets
+// when its parent had already made a cooperative launch before starting it (measured: a child started
+// before the parent's first cooperative launch launches normally), so the text says so.
+int coop_launch(const void* kernel, int nwg, int threads, void** args, unsigned lds, fa_stream_t stream,
+                const char* who);
+
 // Verifies the current device is a 256-CU gfx950 with cooperative launch, raises the
 // kernel's dynamic-LDS limit (once per device and kernel) and checks that `nwg`
 // workgroups of `threads` threads can be co-resident.

@@ -816,8 +816,5 @@ extern "C" int fa_ma2_flow(const fa_ma2_args* a, fa_stream_t stream) {
   p.B = a->batch;
   p.xt_rows = a->xt_rows;
   void* args[] = {&p};
-  hipError_t e = hipLaunchCooperativeKernel(kern, dim3(NWG), dim3(NTHR), args, LDS_BYTES, (hipStream_t)stream);
-  if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_ma2_flow: cooperative launch failed: %s",
-                                         hipGetErrorString(e));
-  return FA_OK;
+  return host::coop_launch(kern, NWG, NTHR, args, LDS_BYTES, stream, "fa_ma2_flow");
 }

@@ -835,11 +835,7 @@ int ma2_bs1_launch(const fa_ma2_args* a, fa_stream_t stream) {
   p.adim = a->adim;
   p.S = a->num_steps;
   void* args[] = {&p};
-  hipError_t e = hipLaunchCooperativeKernel((const void*)ma2x_kernel, dim3(NWG), dim3(NTHR), args, LDS_BYTES,
-                                            (hipStream_t)stream);
-  if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_ma2_flow: cooperative launch failed: %s",
-                                         hipGetErrorString(e));
-  return FA_OK;
+  return host::coop_launch((const void*)ma2x_kernel, NWG, NTHR, args, LDS_BYTES, stream, "fa_ma2_flow");
 }
 
 }  // namespace fa

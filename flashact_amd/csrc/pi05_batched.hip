@@ -392,10 +392,8 @@ int pi05_denoise_batched(const fa_pi05_args* a, fa_stream_t stream) {
   if (rc != FA_OK) return rc;
   if (a->srows > 0 && (rc = pi05_kv_handoff(a, stream)) != FA_OK) return rc;
   void* args[] = {&p};
-  hipError_t e = hipLaunchCooperativeKernel((const void*)pb::pi05_batched_kernel, dim3(NWG), dim3(NTHR), args, LDS_BYTES,
-                                            (hipStream_t)stream);
-  if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_pi05_denoise: batched launch: %s", hipGetErrorString(e));
-  return FA_OK;
+  return host::coop_launch((const void*)pb::pi05_batched_kernel, NWG, NTHR, args, LDS_BYTES, stream,
+                           "fa_pi05_denoise (batched)");
 }
 
 }  // namespace fa

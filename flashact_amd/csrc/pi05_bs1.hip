@@ -425,6 +425,25 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16(unsigned lo, unsigned hi) {
   return u32x4{cvt_fp8x2<false>(lo), cvt_fp8x2<true>(lo), cvt_fp8x2<false>(hi), cvt_fp8x2<true>(hi)};
 }
 
+// Attention operands: bf16, or fp16 when the caller's caches are fp16 (KV16), so the attention runs
+// on the cached keys and values as the caller holds them (v_mfma_f32_16x16x32_f16), with q, this
+// step's keys and values and the softmax weights in fp16 as well.
+template <bool KV16>
+__device__ __forceinline__ unsigned pack_kv(float a, float b) {
+  if constexpr (KV16) return pack_f16x2(a, b);
+  else return pack_bf16x2(a, b);
+}
+template <bool KV16>
+__device__ __forceinline__ unsigned short kv_bits(float a) {
+  if constexpr (KV16) return __builtin_bit_cast(unsigned short, (_Float16)a);
+  else return bf16_bits(a);
+}
+template <bool KV16>
+__device__ __forceinline__ f32x4 mfma_kv(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (KV16) return mfma16h(a, b, c);
+  else return mfma16(a, b, c);
+}
+
 // acc[rt] = sum_k W[row tile rt][k] * X[token 16w+lr][k] over KS k-steps. bf16 weights: fragment
 // F = rt*KS + ks is slot F%16 of ring page pg0 + F/16. fp8 weights: pair P = rt*PRT + ks/2 is slot
 // P%16 of page pg0 + P/16; its 1 KB holds row lr, k 16q..16q+15 of the pair at byte 16 (lr + 16 q),
@@ -655,7 +674,9 @@ __device__ __forceinline__ void stage_norm(const Params& p, const Ctx& c, int bu
 __device__ __forceinline__ f32x4 row_scales(const float* s, size_t row0) { return *reinterpret_cast<const f32x4*>(s + row0); }
 
 // ---------------------------------------------------------------- QKV
-template <bool FP8>
+// q, this step's keys and values: bf16, or fp16 with KV16 (also the rows written into the caller's
+// caches in the last step, which are then the caller's fp16 caches).
+template <bool FP8, bool KV16>
 __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, int pg0, bool last) {
   const int t = 16 * c.wave + c.lr;
   const bool tv = t < p.Tv;
@@ -697,13 +718,13 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
       if (!tv) continue;
       const int d = vr0 - 512;
       // value dims d..d+3 of this step's token t into the XCD's copy: rank t % 32, slot t / 32
-      bf16* vf = reinterpret_cast<bf16*>(p.ws + OFF_VS) + ((c.g * NR + (t & 31)) * 16) * 32 + (t >> 5);
+      unsigned short* vf = reinterpret_cast<unsigned short*>(p.ws + OFF_VS) + ((c.g * NR + (t & 31)) * 16) * 32 + (t >> 5);
 #pragma unroll
-      for (int i = 0; i < 4; i++) vf[(((d + i) & 15) * 16 + ((d + i) >> 4)) * 2] = (bf16)v[i];
+      for (int i = 0; i < 4; i++) vf[(((d + i) & 15) * 16 + ((d + i) >> 4)) * 2] = kv_bits<KV16>(v[i]);
       if (last && c.g == (l & 7)) {
-        bf16* vr = p.vtcache + ((size_t)l * HD + d) * p.Lmax + p.Lp + t;
+        unsigned short* vr = reinterpret_cast<unsigned short*>(p.vtcache) + ((size_t)l * HD + d) * p.Lmax + p.Lp + t;
 #pragma unroll
-        for (int i = 0; i < 4; i++) vr[(size_t)i * p.Lmax] = (bf16)v[i];
+        for (int i = 0; i < 4; i++) vr[(size_t)i * p.Lmax] = kv_bits<KV16>(v[i]);
       }
       continue;
     }
@@ -713,7 +734,7 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
     const float s0 = as_f32(sn[rt][0]), s1 = as_f32(sn[rt][1]);
     const float lo0 = v[0] * c0 - v[1] * s0, hi0 = v[1] * c0 + v[0] * s0;
     const float lo1 = v[2] * c1 - v[3] * s1, hi1 = v[3] * c1 + v[2] * s1;
-    const unsigned plo = pack_bf16x2(lo0, lo1), phi = pack_bf16x2(hi0, hi1);
+    const unsigned plo = pack_kv<KV16>(lo0, lo1), phi = pack_kv<KV16>(hi0, hi1);
     if (vr0 < 256) {
       const uint32_t qb = OFF_Q + c.g * (TP * HD * 2);
       *reinterpret_cast<unsigned*>(p.ws + qb + frag_off(8, t, j)) = plo;
@@ -743,6 +764,7 @@ __device__ __forceinline__ void stage_qkv(const Params& p, const Ctx& c, int l, 
 // loads are issued after the last prefix block's S^T MFMAs (issued with q instead, they keep 48
 // more VGPRs live through the prefix blocks, and the stage measured slower). Keys past kend:
 // S = -inf, V = 0.
+template <bool KV16>
 __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, int pgk) {
   const int C = 32 * max(1, (p.Lp + 32 * NCH - 1) / (32 * NCH));
   const int kbeg = c.kb0, kend = min(kbeg + C, p.Lp);
@@ -817,7 +839,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
       __builtin_amdgcn_sched_barrier(0);  // the tile's fragments are all requested before its MFMAs
       f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 8; ks++) a = mfma16(kf[ks], qf[ks], a);
+      for (int ks = 0; ks < 8; ks++) a = mfma_kv<KV16>(kf[ks], qf[ks], a);
       s[kt] = a;
     }
     if (kb + 32 >= kend) issue_suffix();  // last prefix block: this step's keys arrive under its P V
@@ -846,8 +868,8 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
         pv[i] = exp2_w(s[kt][i] - m);
         psum += pv[i];
       }
-      pk[kt * 2 + 0] = pack_bf16x2(pv[0], pv[1]);
-      pk[kt * 2 + 1] = pack_bf16x2(pv[2], pv[3]);
+      pk[kt * 2 + 0] = pack_kv<KV16>(pv[0], pv[1]);
+      pk[kt * 2 + 1] = pack_kv<KV16>(pv[2], pv[3]);
     }
     psum = cols_sum(psum);
     lsum = lsum * alpha + psum;
@@ -885,7 +907,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
         const int dt = half * 8 + d8;
         const u32x4 va = {vf[d8][0][0] & vm[0][0], vf[d8][0][1] & vm[0][1], vf[d8][1][0] & vm[1][0],
                           vf[d8][1][1] & vm[1][1]};
-        o[dt] = mfma16(va, pb, o[dt] * alpha);
+        o[dt] = mfma_kv<KV16>(va, pb, o[dt] * alpha);
       }
     }
   };
@@ -900,7 +922,7 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
     // and the V^T operand of lane (lr, quarter 0) is dim 16 dt + lr of both slots.
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 8; ks++) a = mfma16(skf[ks], qf[ks], a);
+    for (int ks = 0; ks < 8; ks++) a = mfma_kv<KV16>(skf[ks], qf[ks], a);
     float sv[4], bmax = -1e30f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -919,12 +941,12 @@ __device__ __forceinline__ void stage_att(const Params& p, const Ctx& c, int l, 
     }
     psum = cols_sum(psum);
     lsum = lsum * alpha + psum;
-    const u32x4 pb = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), 0u, 0u};
+    const u32x4 pb = {pack_kv<KV16>(pv[0], pv[1]), pack_kv<KV16>(pv[2], pv[3]), 0u, 0u};
     const unsigned slot_mask = nsfx == 2 ? 0xffffffffu : 0xffffu;  // slot 1 is stale without token r + 32
 #pragma unroll
     for (int dt = 0; dt < 16; dt++) {
       const u32x4 va = {svf[dt >> 2][dt & 3] & slot_mask, 0u, 0u, 0u};
-      o[dt] = mfma16(va, pb, o[dt] * alpha);
+      o[dt] = mfma_kv<KV16>(va, pb, o[dt] * alpha);
     }
   }
   stamp(c, 24);
@@ -1145,7 +1167,7 @@ __device__ __forceinline__ void mark(const Params& p, const Ctx& c, int idx, uin
 }
 
 // ---------------------------------------------------------------- kernel
-template <bool FP8>
+template <bool FP8, bool KV16>
 __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
   using PG = Pages<FP8>;
   Ctx c;
@@ -1226,14 +1248,14 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       launder(c);
       mark(p, c, 9, t0);
       stamp(c, 2);
-      stage_qkv<FP8>(p, c, l, pb + PG::QKV, step == p.S - 1);
+      stage_qkv<FP8, KV16>(p, c, l, pb + PG::QKV, step == p.S - 1);
       stamp(c, 3);
       mark(p, c, 1, t0);
       xcd_sync(p, c);
       launder(c);
       mark(p, c, 9, t0);
       stamp(c, 4);
-      stage_att(p, c, l, pb + PG::K);
+      stage_att<KV16>(p, c, l, pb + PG::K);
       stamp(c, 5);
       mark(p, c, 2, t0);
       xcd_sync(p, c);
@@ -1322,7 +1344,7 @@ int fa::pi05_bs1_coop_capacity(int device) {
   if (hipGetDevice(&prev) != hipSuccess) return 0;
   if (device != prev && hipSetDevice(device) != hipSuccess) return 0;
   int per_cu = 0, cus = 0;
-  const void* kern = (const void*)pi05::pi05_denoise_bs1<false>;
+  const void* kern = (const void*)pi05::pi05_denoise_bs1<false, false>;
   if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pi05::LDS_BYTES) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, pi05::NTH, pi05::LDS_BYTES) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
@@ -1402,9 +1424,12 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: KV cache larger than 2 GiB per sample");
   if (a->xt_rows < a->Tv)
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: xt_rows=%d < Tv=%d", a->xt_rows, a->Tv);
-  if (a->cache_dtype == FA_DTYPE_F16) {
-    // The reference's fp16 caches: import into the bf16 shadow, run the bf16 loop on it, export the
-    // rows the loop wrote. Stream order sequences the three.
+  // The reference's fp16 caches at batch 1 without a hand-off: the batch-1 kernel reads and writes
+  // them as they are and runs its attention in fp16 (no shadow).
+  const bool kv16 = a->cache_dtype == FA_DTYPE_F16 && a->batch == 1 && a->srows == 0;
+  if (a->cache_dtype == FA_DTYPE_F16 && !kv16) {
+    // fp16 caches elsewhere (batch >= 2, or a hand-off): import into the bf16 shadow, run the bf16
+    // loop on it, export the rows the loop wrote. Stream order sequences the three.
     const size_t need = fa_pi05_cache_shadow_bytes(a->batch, a->num_layers, a->Lmax);
     if (!a->cache_shadow || (reinterpret_cast<uintptr_t>(a->cache_shadow) & 255) || a->cache_shadow_bytes < need)
       return host::fail(FA_ERR_INVALID_ARG,
@@ -1422,14 +1447,15 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
     if (rc == FA_OK) rc = pi05_cache_export(a, stream);
     return rc;
   }
-  if (a->cache_dtype != FA_DTYPE_BF16)
+  if (a->cache_dtype != FA_DTYPE_BF16 && !kv16)
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: cache_dtype=%d is neither FA_DTYPE_BF16 nor FA_DTYPE_F16",
                       a->cache_dtype);
   if (a->batch > 1) return pi05_denoise_batched(a, stream);
   if (a->workspace_bytes < WS_BYTES)
     return host::fail(FA_ERR_INVALID_ARG, "fa_pi05_denoise: workspace_bytes=%zu < required %u", a->workspace_bytes,
                       (unsigned)WS_BYTES);
-  const void* kern = fp8 ? (const void*)pi05_denoise_bs1<true> : (const void*)pi05_denoise_bs1<false>;
+  const void* kern = fp8 ? (kv16 ? (const void*)pi05_denoise_bs1<true, true> : (const void*)pi05_denoise_bs1<true, false>)
+                         : (kv16 ? (const void*)pi05_denoise_bs1<false, true> : (const void*)pi05_denoise_bs1<false, false>);
   int rc = host::check_device(kern, NTH, LDS_BYTES, NWG, "fa_pi05_denoise");
   if (rc != FA_OK) return rc;
 
@@ -1465,11 +1491,7 @@ extern "C" int fa_pi05_denoise(const fa_pi05_args* a, fa_stream_t stream) {
   p.xt_rows = a->xt_rows;
   if (a->srows > 0 && (rc = pi05_kv_handoff(a, stream)) != FA_OK) return rc;
   void* args[] = {&p};
-  hipError_t e = hipLaunchCooperativeKernel(kern, dim3(NWG), dim3(NTH), args, LDS_BYTES,
-                                            (hipStream_t)stream);
-  if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_pi05_denoise: cooperative launch failed: %s",
-                                         hipGetErrorString(e));
-  return FA_OK;
+  return host::coop_launch(kern, NWG, NTH, args, LDS_BYTES, stream, "fa_pi05_denoise");
 }
 
 // ---------------------------------------------------------------- no-allocation variant

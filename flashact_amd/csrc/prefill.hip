@@ -396,8 +396,5 @@ extern "C" int fa_pi05_prefill(const fa_prefill_args* a, fa_stream_t stream) {
   p.Tv = a->Lp;
   p.B = a->batch;
   void* args[] = {&p};
-  hipError_t e = hipLaunchCooperativeKernel((const void*)prefill_kernel, dim3(NWG), dim3(NTHR), args, LDS_BYTES,
-                                            (hipStream_t)stream);
-  if (e != hipSuccess) return host::fail(FA_ERR_LAUNCH, "fa_pi05_prefill: launch: %s", hipGetErrorString(e));
-  return FA_OK;
+  return host::coop_launch((const void*)prefill_kernel, NWG, NTHR, args, LDS_BYTES, stream, "fa_pi05_prefill");
 }

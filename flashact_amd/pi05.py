@@ -260,8 +260,9 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
       * weights are bf16 ([NL][2560][1024] ... as packed by ``pack_weights``) with s1..s3 empty/None,
         or FP8-W8A16 (batch 1): e4m3 codes (uint8 or float8_e4m3fn) with fp32 per-row scales s1..s3,
         as ``pack_weights_fp8`` makes them (the reference's quantisation);
-      * kcache/vtcache are bf16, or fp16 as the reference allocates them: the C ABI then runs on a
-        bf16 shadow (``cache_shadow()``) and writes the rows it produced back in fp16;
+      * kcache/vtcache are bf16, or fp16 as the reference allocates them: at batch 1 (srows = 0) the
+        loop runs its attention in fp16 on them directly; otherwise the C ABI runs on a bf16 shadow
+        (``cache_shadow()``) and writes the rows it produced back in fp16;
       * the scratch tensors x, xp, xn, q, attn, hmlp, scores, probs are accepted and ignored: the
         MI355X engine keeps its intermediates in one workspace (``workspace()``);
       * nblocks/nthreads are ignored: the grid is one workgroup per CU (256);
@@ -324,8 +325,10 @@ def launch(w1, wo, w2, w3, s1, so_, s2, s3, mods, mod_final, rope_cos, rope_sin,
             raise TypeError("trace must be an int64 tensor with >= 256*6*32 entries")
         a.trace, a.trace_layer = _ptr(trace), int(trace_layer)
     if kcache.dtype == torch.float16:
-        sh = cache_shadow(dev, batch, nl, Lmax)
-        a.cache_dtype, a.cache_shadow, a.cache_shadow_bytes = _lib.FA_DTYPE_F16, sh.data_ptr(), sh.numel()
+        a.cache_dtype = _lib.FA_DTYPE_F16
+        if batch > 1 or srows > 0:  # batch 1 without a hand-off runs on the fp16 caches directly
+            sh = cache_shadow(dev, batch, nl, Lmax)
+            a.cache_shadow, a.cache_shadow_bytes = sh.data_ptr(), sh.numel()
     stream = torch.cuda.current_stream(dev)
     _lib.check(L.fa_pi05_denoise(ctypes.byref(a), ctypes.c_void_p(stream.cuda_stream)), "fa_pi05_denoise")
     if check_status:

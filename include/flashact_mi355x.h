@@ -130,13 +130,17 @@ typedef struct fa_pi05_args {
    * layer's weight pages was issued and landed: trace [256 workgroups][6][32]. NULL disables. */
   unsigned long long* trace;
   int trace_layer;
-  /* Cache element type: FA_DTYPE_BF16 (0), or FA_DTYPE_F16 for the reference's fp16 caches. With
-   * fp16 caches the launch converts both caches to bf16 into cache_shadow (at least
-   * fa_pi05_cache_shadow_bytes(batch, num_layers, Lmax) bytes, 256-byte aligned, caller-owned),
-   * runs the loop on the shadow (the hand-off, srows > 0, writes it too) and converts the rows it
-   * wrote back into the caller's fp16 caches: [Lp, Lp+Tv), and [0, Lp) as well with srows > 0.
-   * fp16 -> bf16 rounds each cached value to 8 significant bits, as the bf16 operands of the
-   * attention MFMAs would. cache_shadow is ignored for bf16 caches. */
+  /* Cache element type: FA_DTYPE_BF16 (0), or FA_DTYPE_F16 for the reference's fp16 caches.
+   * fp16 caches at batch 1 with srows == 0 (the reference's own call): the loop reads and writes
+   * them directly and runs its attention in fp16 (q, this step's keys and values, the softmax weights
+   * and the cached keys and values as fp16 MFMA operands, as src/pi05/mk6.cu computes it);
+   * cache_shadow is then not used and may be NULL.
+   * fp16 caches otherwise (batch >= 2, or a hand-off with srows > 0): the launch converts both
+   * caches to bf16 into cache_shadow (at least fa_pi05_cache_shadow_bytes(batch, num_layers, Lmax)
+   * bytes, 256-byte aligned, caller-owned), runs the loop on the shadow (the hand-off writes it too)
+   * and converts the rows it wrote back into the caller's fp16 caches: [Lp, Lp+Tv), and [0, Lp) as
+   * well with srows > 0; fp16 -> bf16 rounds each cached value to 8 significant bits, as the bf16
+   * operands of the attention MFMAs would. cache_shadow is ignored for bf16 caches. */
   int cache_dtype;
   void* cache_shadow;
   size_t cache_shadow_bytes;

@@ -118,3 +118,18 @@ def test_cpp_driver_ma2(drivers):
     assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
     assert np.all(xo[Tv:] == 0.0)
     assert np.array_equal(xo[:Tv, adim:], c["inp"]["noise"][0, :, adim:].numpy())
+
+
+def test_child_after_parent_launch_is_refused_with_a_clear_error(tmp_path, gpu):
+    """A child process started after this process has made cooperative launches (every earlier GPU
+    test did): where the runtime refuses the child's cooperative launch (hipErrorIllegalState, seen on
+    these boxes), fa_last_error() must say why and what to do instead of a bare launch failure. Where
+    the runtime allows it, the child simply succeeds. No kernel runs in the refused case."""
+    c = P.make_case(NL=1, Lp=40, Tv=10, S=1, seed=3)
+    P.run_gpu(c, gpu)  # this process's own cooperative launch, in case this test runs alone
+    d = str(tmp_path)
+    _, _, args = _pi05_files(d)
+    res = subprocess.run([DRIVER_PATH, *map(str, args)], capture_output=True, text=True, timeout=120)
+    print("child rc", res.returncode, res.stderr.strip()[-400:], flush=True)
+    if res.returncode != 0:
+        assert "refused the cooperative launch" in res.stderr and "parent" in res.stderr, res.stderr

@@ -4,11 +4,13 @@ benchmarks/pi05/eval_numerics.py:71-107 builds: per-row e4m3 codes (uint8) with 
 fp16 caches kcache [NL][Lmax][256] / vtcache [NL][256][Lmax] with Lmax = ceil16(Lp + T), x_t of
 T = 16 rows of which Tv = 10 are valid, the fp32 / fp16 scratch tensors x, xp, xn, q, attn, hmlp,
 scores, probs, an int64 stage counter, empty bf16 hand-off tensors with srows = 0, and 170 x 256
-threads; then calls ``launch`` with them in that order. The same call here must match the
-oracle's fp8 loop on the same codes, scales and the caller's fp16 cache values as they are (the
-oracle reads the fp16 bits; nothing is rounded for it), write the suffix rows back into the fp16
-caches, and leave rows [Tv, T) of x_t alone. Each launch starts from a freshly initialised
-workspace, so a comparison of two launches does not depend on the workspace's exchange history.
+threads; then calls ``launch`` with them in that order. The same call here runs the batch-1 loop
+directly on the fp16 caches with its attention in fp16 (as src/pi05/mk6.cu:35, 95-101 computes it),
+must match the oracle's fp8 loop on the same codes, scales and the caller's fp16 cache values as
+they are (the oracle reads the fp16 bits; nothing is rounded for it), write the suffix rows back into
+the fp16 caches, and leave rows [Tv, T) of x_t alone. The same values in bf16 caches (each rounded to
+8 significant bits) run the bf16 attention; both errors are printed side by side. Each launch starts
+from a freshly initialised workspace, so the comparison does not depend on the workspace's history.
 """
 import numpy as np
 import pytest
@@ -84,14 +86,13 @@ def test_reference_call_fp8_fp16_caches(gpu):
     ow["vpre"] = vh.numpy().view(np.uint16)
     ref = O.pi05_denoise_fp8(ow, c["inp"]["noise"].numpy(), Lp=Lp, Tv=TV, S=S, NL=NL, kv_dtype="f16")[0]
     st = P.parity(out[:TV], ref)
-    print(f"reference call (fp8 codes, fp16 caches, T=16, Tv=10, 18 layers x 10 steps) vs the oracle on the "
-          f"fp16 cache values: {st}", flush=True)
+    print(f"reference call (fp8 codes, fp16 caches, T=16, Tv=10, 18 layers x 10 steps), fp16 attention, vs the "
+          f"oracle on the fp16 cache values: {st}", flush=True)
     assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
     assert np.all(out[TV:] == 0.0), "rows [Tv, T) of x_t must be left untouched"
     assert int(sc_cyc.sum()) > 0
 
-    # the prefix rows of the fp16 caches are untouched; the suffix rows hold this call's keys and
-    # values, identical (after fp16 rounding) to a launch on bf16 caches of the same values
+    # the same cache values in bf16 caches (rounded to 8 significant bits): the bf16 attention
     kb, vb = _caches(kh, vh, Lmax, torch.bfloat16, dev)
     kb, vb = kb[0].contiguous(), vb[0].contiguous()
     x2 = torch.zeros(T, AD, dtype=torch.float32, device=dev)
@@ -101,10 +102,17 @@ def test_reference_call_fp8_fp16_caches(gpu):
                 mods, modf, cos, sin, wv["w_ain"], wv["b_ain"], wv["w_aout"], wv["b_aout"],
                 empty, empty, 0, kb, vb, Lp, Lmax, S, TV, x2)
     torch.cuda.synchronize()
-    assert torch.equal(x2, x_t), "fp16 caches must give the bf16-cache result on the same (rounded) values"
+    st2 = P.parity(x2[:TV].cpu().numpy(), ref)
+    print(f"the same call on bf16 caches of the same values (bf16 attention): {st2}", flush=True)
+    assert st2["max_abs"] <= MAX_ABS and st2["mean_abs"] <= MEAN_ABS, st2
+    # the prefix rows of the fp16 caches are untouched; the suffix rows hold this call's keys and
+    # values in fp16, within bf16 rounding of the bf16 launch's rows (the two loops' states differ by
+    # their attention precision only)
     assert torch.equal(kcache[:, :Lp].cpu(), kh[0]) and torch.equal(vtcache[:, :, :Lp].cpu(), vh[0].transpose(1, 2))
-    assert torch.equal(kcache[:, Lp:Lp + TV], kb[:, Lp:Lp + TV].half())
-    assert torch.equal(vtcache[:, :, Lp:Lp + TV], vb[:, :, Lp:Lp + TV].half())
+    for a16, b16 in ((kcache[:, Lp:Lp + TV].float(), kb[:, Lp:Lp + TV].float()),
+                     (vtcache[:, :, Lp:Lp + TV].float(), vb[:, :, Lp:Lp + TV].float())):
+        assert torch.count_nonzero(a16) == a16.numel()
+        assert float((a16 - b16).abs().max()) <= 0.02 * float(b16.abs().max()) + 1e-3
     assert torch.count_nonzero(kcache[:, Lp + TV:]) == 0
 
 
@@ -130,3 +138,32 @@ def test_fp16_caches_batched(gpu):
     assert torch.equal(a[0], b[0])
     assert torch.equal(a[1][:, :, Lp:Lp + TV], b[1][:, :, Lp:Lp + TV].half())
     assert torch.equal(a[2][..., Lp:Lp + TV], b[2][..., Lp:Lp + TV].half())
+
+
+@pytest.mark.parametrize("NL,Lp,Tv,S", [(2, 968, 50, 2), (2, 0, 17, 2), (1, 2003, 33, 2), (2, 37, 1, 3), (18, 968, 50, 10)])
+def test_fp16_caches_batch1_bf16_weights(gpu, NL, Lp, Tv, S):
+    """Batch 1 on fp16 caches with bf16 weights: the fp16 attention against the oracle reading the
+    same fp16 cache values (Lp = 2003: the keys past each rank's first 32 come from the caches; Lp = 0:
+    this step's keys only)."""
+    c = P.make_case(NL=NL, Lp=Lp, Tv=Tv, S=S, seed=40 + Lp + Tv)
+    g = P.gpu_tensors(c, gpu)
+    Lmax = g["Lmax"]
+    kh, vh = _fp16_caches(NL, Lp, Lmax, seed=41 + Lp)
+    kc, vc = _caches(kh, vh, Lmax, torch.float16, gpu)
+    kc, vc = kc[0].contiguous(), vc[0].contiguous()
+    p = g["packed"]
+    x_t = c["inp"]["noise"][0].to(gpu).clone()
+    empty = torch.empty(0, device=gpu)
+    pi05.reset_workspace(pi05.workspace(gpu))
+    pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], empty, empty, empty, empty, g["mods"], g["mod_final"],
+                g["cos"], g["sin"], g["w_ain"], g["b_ain"], g["w_aout"], g["b_aout"], None, None, 0,
+                kc, vc, Lp, Lmax, S, Tv, x_t, check_status=True)
+    from oracle import oracle as O
+    ow = P.oracle_weights(c)
+    ow["kpre"], ow["vpre"] = kh.numpy().view(np.uint16), vh.numpy().view(np.uint16)
+    ref = O.pi05_denoise(ow, c["inp"]["noise"].numpy(), Lp=Lp, Tv=Tv, S=S, NL=NL, kv_dtype="f16")[0]
+    st = P.parity(x_t.cpu().numpy(), ref)
+    print(f"fp16 caches, bf16 weights NL={NL} Lp={Lp} Tv={Tv} S={S}: {st}", flush=True)
+    assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
+    assert torch.equal(kc[:, :Lp].cpu(), kh[0][:, :Lp])
+    assert torch.count_nonzero(kc[:, Lp:Lp + Tv]) == kc[:, Lp:Lp + Tv].numel()

@@ -199,16 +199,29 @@ def _c_args(**kw):
     return a
 
 
+# fp16 caches need the bf16 shadow only where the loop does not run on them directly: batch >= 2 or
+# a hand-off (srows > 0)
 @pytest.mark.parametrize("kw,text", [
-    (dict(cache_dtype=_lib.FA_DTYPE_F16), "cache_shadow"),
-    (dict(cache_dtype=_lib.FA_DTYPE_F16, cache_shadow=(1 << 20) + 16, cache_shadow_bytes=1 << 30), "cache_shadow"),
-    (dict(cache_dtype=_lib.FA_DTYPE_F16, cache_shadow=1 << 20, cache_shadow_bytes=1 << 20), "cache_shadow"),
+    (dict(cache_dtype=_lib.FA_DTYPE_F16, batch=2), "cache_shadow"),
+    (dict(cache_dtype=_lib.FA_DTYPE_F16, srows=968, kvsrc_k=1 << 20, kvsrc_v=1 << 21), "cache_shadow"),
+    (dict(cache_dtype=_lib.FA_DTYPE_F16, batch=2, cache_shadow=(1 << 20) + 16, cache_shadow_bytes=1 << 30),
+     "cache_shadow"),
+    (dict(cache_dtype=_lib.FA_DTYPE_F16, batch=2, cache_shadow=1 << 20, cache_shadow_bytes=1 << 20), "cache_shadow"),
     (dict(cache_dtype=7), "cache_dtype"),
 ])
 def test_c_abi_fp16_cache_validation(kw, text):
     L = _lib.lib()
     rc = L.fa_pi05_denoise(ctypes.byref(_c_args(**kw)), None)
     assert rc == 1 and text in L.fa_last_error().decode()
+
+
+def test_c_abi_fp16_caches_at_batch_1_need_no_shadow():
+    """The reference's own call (batch 1, no hand-off) runs on the fp16 caches: no shadow is asked for,
+    and the request gets as far as the device check (there is no GPU here)."""
+    L = _lib.lib()
+    rc = L.fa_pi05_denoise(ctypes.byref(_c_args(cache_dtype=_lib.FA_DTYPE_F16)), None)
+    err = L.fa_last_error().decode()
+    assert "cache_shadow" not in err and rc != 0
 
 
 def test_cache_shadow_bytes():

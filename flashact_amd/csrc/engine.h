@@ -132,10 +132,13 @@ __device__ __forceinline__ void grid_sync(Grid& g) {
   __syncthreads();
   g.e += 1;
   const int x = blockIdx.x & 7, rk = blockIdx.x >> 3, lane = threadIdx.x & 63;
+  // flag stores through a wave-uniform descriptor (a generic pointer would keep the 64-bit address in
+  // VGPRs across the whole layer loop)
+  const rsrc_t r = make_rsrc(g.flags, 4096);
+  const u32x2 ev = {(unsigned)g.e, (unsigned)(g.e >> 32)};
   if (threadIdx.x == 0)  // this XCD's slot (plain store: read back from the XCD's L2 by its leader)
-    __hip_atomic_store(g.flags + x * 32 + rk, g.e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    stb64<kCpPlain>(r, (uint32_t)(x * 32 + rk) * 8, ev);
   if (threadIdx.x < 64 && !(__hip_atomic_load(g.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin)) {
-    const rsrc_t r = make_rsrc(g.flags, 4096);
     auto wait = [&](bool mine, uint32_t off) {
       for (unsigned it = 0;; ++it) {
         const u32x2 v = ldb64<kCpSc1>(r, mine ? off : 0x80000000u);
@@ -149,10 +152,9 @@ __device__ __forceinline__ void grid_sync(Grid& g) {
     };
     if (rk == 0) {  // XCD leader: its 32 workgroups, then the 8 XCD leaders, then release its XCD
       wait(lane < 32, (uint32_t)(x * 32 + lane) * 8);
-      if (lane == 0) __hip_atomic_store(g.flags + 256 + x, g.e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) stb64<kCpSc1>(r, (uint32_t)(256 + x) * 8, ev);  // read by the other XCDs' leaders
       wait(lane < 8, (uint32_t)(256 + lane) * 8);
-      if (lane == 0)
-        __hip_atomic_store(g.flags + 384 + 16 * x, g.e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (lane == 0) stb64<kCpPlain>(r, (uint32_t)(384 + 16 * x) * 8, ev);
     } else {
       wait(lane == 0, (uint32_t)(384 + 16 * x) * 8);
     }

@@ -122,6 +122,11 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
   const Layout& L = p.L;
   const int lane = lane_id();
   const int nwave = NWG * 4;
+  // wave-uniform descriptors with 32-bit lane offsets (per-lane 64-bit pointers cost two VGPRs each,
+  // which the compiler kept live across the layer loop and spilled)
+  const rsrc_t rg = make_rsrc(gate, gate ? D * 4 : 0), rsc = make_rsrc(scale, D * 4), rsh = make_rsrc(shift, D * 4);
+  const rsrc_t rbi = make_rsrc(p.b_ain, D * 4), rwi = make_rsrc(p.w_ain, D * AD * 4);
+  const rsrc_t rwo = make_rsrc(p.w_aout, AD * D * 4), rbo = make_rsrc(p.b_aout, AD * 4);
 #pragma unroll 1
   for (int m = vwg() * 4 + wave_id(); m < L.M; m += nwave) {
     const int b = m / p.Tv, t = m - b * p.Tv;
@@ -135,13 +140,13 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         const int d = 4 * lane + 256 * k;
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(p.b_ain + d);
+        const f32x4 bb = as_f32x4(ldb128<kCpPlain>(rbi, d * 4));
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           float s = bb[i];
 #pragma unroll
           for (int q = 0; q < 8; q++) {
-            const f32x4 wv = *reinterpret_cast<const f32x4*>(p.w_ain + (d + i) * AD + 4 * q);
+            const f32x4 wv = as_f32x4(ldb128<kCpPlain>(rwi, ((d + i) * AD + 4 * q) * 4));
 #pragma unroll
             for (int e = 0; e < 4; e++) s = fmaf(wv[e], xa[4 * q + e], s);
           }
@@ -164,7 +169,7 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
         f32x4 s = as_f32x4(pr[0][k]);
 #pragma unroll
         for (int sp = 1; sp < KSPLIT; sp++) s += as_f32x4(pr[sp][k]);
-        const f32x4 gt = *reinterpret_cast<const f32x4*>(gate + d);
+        const f32x4 gt = as_f32x4(ldb128<kCpPlain>(rg, d * 4));
         x[k] = as_f32x4(xo[k]) + gt * s;
       }
     }
@@ -176,8 +181,8 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int d = 4 * lane + 256 * k;
-      const f32x4 sc = *reinterpret_cast<const f32x4*>(scale + d);
-      const f32x4 sh = *reinterpret_cast<const f32x4*>(shift + d);
+      const f32x4 sc = as_f32x4(ldb128<kCpPlain>(rsc, d * 4));
+      const f32x4 sh = as_f32x4(ldb128<kCpPlain>(rsh, d * 4));
 #pragma unroll
       for (int i = 0; i < 4; i++) h[k][i] = x[k][i] * rr * (1.0f + sc[i]) + sh[i];
     }
@@ -205,7 +210,7 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
         for (int a = 0; a < 8; a++)
 #pragma unroll
           for (int k = 0; k < 4; k++)
-            wv[a][k] = *reinterpret_cast<const f32x4*>(p.w_aout + (a0 + a) * D + 4 * lane + 256 * k);
+            wv[a][k] = as_f32x4(ldb128<kCpPlain>(rwo, ((a0 + a) * D + 4 * lane + 256 * k) * 4));
 #pragma unroll
         for (int a = 0; a < 8; a++) {
           float s = 0.f;
@@ -218,7 +223,8 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
       }
       if (lane < AD) {
         const float xo = ldbf32<kCpSc1>(xtr, xto + lane * 4);
-        __builtin_amdgcn_raw_buffer_store_b32(as_u32(xo + dt * (acc + p.b_aout[lane])), xtr, xto + lane * 4, 0, kCpSc1);
+        __builtin_amdgcn_raw_buffer_store_b32(as_u32(xo + dt * (acc + ldbf32<kCpPlain>(rbo, lane * 4))), xtr, xto + lane * 4,
+                                              0, kCpSc1);
       }
     }
   }

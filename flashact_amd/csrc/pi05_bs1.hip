@@ -12,9 +12,10 @@
 //   O and down projections. Per layer (sync after each stage in brackets):
 //     N1 [X] QKV [X] ATT [X] COMB [X] O {exchange} N2 [X] GU [X] DN {exchange}
 //   [X] = XCD sync point: every compute wave of the XCD stores its epoch to its own flag slot. Before
-//         ATT and COMB (whose waves read every rank's output) each wave polls the XCD's 128 slots;
-//         before QKV, O, GU and DN each wave polls only the waves that wrote its operand rows
-//         (DN: one group of 16 gate/up ranks per 8-k-step chunk of its K loop).
+//         ATT (whose waves read q and this step's keys from every QKV rank) each wave polls the
+//         XCD's 128 slots; before QKV, COMB, O, GU and DN each wave polls only the waves that wrote
+//         its operands (COMB: the 8 attention ranks of its chunks; DN: one group of 16 gate/up ranks
+//         per 8-k-step chunk of its K loop).
 //   {exchange} = the O / down partial sums are the only data crossing XCDs. Producers store
 //         them as fp16 (half the bytes of fp32: the exchange is partly bandwidth-bound) with the
 //         exchange parity in the lowest mantissa bit of every value; the
@@ -34,7 +35,8 @@
 //        O^T = V^T P^T; normalised partial O (bf16, whole operand fragments) with (m, l) per
 //        chunk.
 //   COMB: flash-decoding combine of the 32 chunk partials, one operand fragment of attn_g per
-//        rank (four waves, eight chunks each, meeting in LDS).
+//        rank (four waves, eight chunks each, meeting in LDS); a wave waits only for the attention
+//        waves of its eight chunks.
 //   O:   W_o[32r..32r+32, 256g..256g+256) x attn_g -> partial o_g.
 //   GU:  32 interleaved gate/up rows per CU -> gelu_tanh(g)*u -> h_g (bf16, XCD-private).
 //   DN:  W_d[32r..32r+32, 512g..512g+512) x h_g -> partial z_g.
@@ -987,6 +989,7 @@ __device__ __forceinline__ void stage_comb(const Params& p, const Ctx& c, int li
   if (16 * tt >= p.Tv) return;
   const int t = 16 * tt + (c.lane >> 2);
   constexpr int NC = NCH / NCW;
+  xcd_wait_ranks(c, NC * c.wave, NC, tt);  // the attention waves of this wave's chunks
   u32x4 v[NC];
   u32x2 ml[NC];
 #pragma unroll
@@ -1258,7 +1261,7 @@ __global__ void __launch_bounds__(NTH, 1) pi05_denoise_bs1(Params p) {
       stage_att<KV16>(p, c, l, pb + PG::K);
       stamp(c, 5);
       mark(p, c, 2, t0);
-      xcd_sync(p, c);
+      xcd_signal(p, c);  // combine waves wait for the attention waves of their chunks
       launder(c);
       mark(p, c, 9, t0);
       stamp(c, 6);

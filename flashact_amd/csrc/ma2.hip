@@ -54,7 +54,8 @@ __host__ __device__ inline int pick_ks(int nm, int nn, int K) {
   return best;
 }
 
-__host__ __device__ inline Layout layout(int B, int Tv, int Lkmax, int BM, int BN) {
+// BM x BN tiles for every GEMM but gate/up, BM x BNG for gate/up.
+__host__ __device__ inline Layout layout(int B, int Tv, int Lkmax, int BM, int BN, int BNG) {
   Layout L;
   L.B = B;
   L.Tv = Tv;
@@ -64,7 +65,7 @@ __host__ __device__ inline Layout layout(int B, int Tv, int Lkmax, int BM, int B
   const int nm = L.MP / BM;
   L.ks_qkv = pick_ks(nm, QKVN / BN, D);
   L.ks_d = pick_ks(nm, D / BN, D);
-  L.ks_gu = pick_ks(nm, GUN / BN, D);
+  L.ks_gu = pick_ks(nm, GUN / BNG, D);
   L.ks_dn = pick_ks(nm, D / BN, FF);
   const int ks_part = L.ks_d > L.ks_dn ? L.ks_d : L.ks_dn;
   size_t o = kWsDataBase;  // control words, epoch flags and the fixup counters below
@@ -84,7 +85,7 @@ __host__ __device__ inline Layout layout(int B, int Tv, int Lkmax, int BM, int B
   L.yqkv = take((size_t)L.MP * QKVN * 4);
   L.yq = take((size_t)L.MP * D * 4);
   L.yo = take((size_t)L.MP * D * 4);
-  L.ntiles = nm * (GUN / BN);
+  L.ntiles = nm * (GUN / BNG);
   L.cnt = kWsCounters;  // fixed: never moves with the shape, so a reused workspace keeps them zero
   L.cattp = take((size_t)B * NH * L.NKC * MAX_TV * HD * 2);
   L.cml = take((size_t)B * NH * L.NKC * MAX_TV * 8);
@@ -596,9 +597,10 @@ __device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {
   }
 }
 
-template <int WM, int WN>
+// (32 WM) x (32 WN) tiles for every GEMM but gate/up, (32 WM) x (32 WNG) for gate/up.
+template <int WM, int WN, int WNG>
 __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
-  static_assert(GemmShape<WM, WN>::LDS <= RING_BYTES, "LDS budget");
+  static_assert(GemmShape<WM, WN>::LDS <= RING_BYTES && GemmShape<WM, WNG>::LDS <= RING_BYTES, "LDS budget");
   const Layout& L = p.L;
   const rsrc_t ws = rsrc_all(p.ws);
   const rsrc_t xtr = make_rsrc(p.x_t, (uint32_t)((size_t)p.B * p.xt_rows * AD * 4));
@@ -680,14 +682,14 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
       gx.W = p.w_gu + (size_t)l * GUN * D;
       if constexpr (FIX) {
         FinSiluGate f{ws, (uint32_t)L.h, p.b_gu + (size_t)l * GUN};
-        gemm_stage_fixup<WM, WN, true>(gx, GUN, D, L.ks_gu, ws, (uint32_t)L.pgu, L.MP, cnt, RING_BYTES, f);
+        gemm_stage_fixup<WM, WNG, true>(gx, GUN, D, L.ks_gu, ws, (uint32_t)L.pgu, L.MP, cnt, RING_BYTES, f);
       } else if (L.ks_gu == 1) {  // one pass of tiles covers the grid: gate fused into the epilogue
         EpiSiluGate e{ws, (uint32_t)L.h, p.b_gu + (size_t)l * GUN, 0};
-        gemm_stage<WM, WN, true>(gx, GUN, D, 1, e);
+        gemm_stage<WM, WNG, true>(gx, GUN, D, 1, e);
         mark(p, 10, t0);
       } else {
         EpiPartN e{{}, ws, (uint32_t)L.pgu, L.MP, GUN, 0};
-        gemm_stage<WM, WN, true>(gx, GUN, D, L.ks_gu, e);
+        gemm_stage<WM, WNG, true>(gx, GUN, D, L.ks_gu, e);
         sync(10);
         stage_gate(p, ws, l);
       }
@@ -707,9 +709,18 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Tile shapes: batches of up to 64 tokens use 32-token x 64-row tiles, larger ones 128 x 128.
+// Tile shapes: batches of up to 64 tokens use 32-token x 64-row tiles; larger ones 128 x 64 tiles,
+// except gate/up on 128 x 128. At batch 16 (480 tokens) the 128 x 64 tiles need no K split for QKV
+// (144 tiles) and half the splits elsewhere (down 4 instead of 8, the 768 x 768 projections 3 instead
+// of 6), so the stages that sum the partials read fewer of them. Per layer at batch 16 against
+// 128 x 128 everywhere: QKV + SATT 13.4 -> 13.1, SO + N_mca 10.6 -> 8.8, CQ 5.3 -> 4.2, CO + N_mlp
+// 10.5 -> 8.6, DN + N_msa 14.0 -> 13.9 us; 38.3 -> 36.1 ms per launch. Gate/up stays on 128 x 128
+// (16.1 us per layer on 128 x 64 against 11.0).
 constexpr int SMALL_M = 64;
 __host__ inline bool small_cfg(int M) { return M <= SMALL_M; }
+__host__ inline Layout layout_for(int B, int Tv, int Lkmax) {
+  return small_cfg(B * Tv) ? layout(B, Tv, Lkmax, 32, 64, 64) : layout(B, Tv, Lkmax, 128, 64, 128);
+}
 
 }  // namespace ma2
 }  // namespace fa
@@ -720,8 +731,7 @@ using namespace fa;
 extern "C" size_t fa_ma2_workspace_bytes(int batch, int Tv, int Lkmax) {
   if (batch < 1 || Tv < 1 || Tv > ma2::MAX_TV || Lkmax < 16 || (size_t)batch * Tv > (size_t)ma2::MAX_TOKENS) return 0;
   if (ma2_bs1_eligible(batch, Tv, Lkmax)) return ma2_bs1_workspace_bytes();
-  const bool sm = ma2::small_cfg(batch * Tv);
-  const size_t n = ma2::layout(batch, Tv, Lkmax, sm ? 32 : 128, sm ? 64 : 128).total;
+  const size_t n = ma2::layout_for(batch, Tv, Lkmax).total;
   return n < 0xffffffffull ? n : 0;
 }
 
@@ -775,7 +785,7 @@ extern "C" int fa_ma2_flow(const fa_ma2_args* a, fa_stream_t stream) {
                       need);
   if (ma2_bs1_eligible(a->batch, a->Tv, a->Lkmax)) return ma2_bs1_launch(a, stream);
   const bool sm = small_cfg(a->batch * a->Tv);
-  const void* kern = sm ? (const void*)ma2_kernel<1, 2> : (const void*)ma2_kernel<4, 4>;
+  const void* kern = sm ? (const void*)ma2_kernel<1, 2, 2> : (const void*)ma2_kernel<4, 2, 4>;
   int rc = host::check_device(kern, NTHR, LDS_BYTES, NWG, "fa_ma2_flow");
   if (rc != FA_OK) return rc;
   Params p;
@@ -804,7 +814,7 @@ extern "C" int fa_ma2_flow(const fa_ma2_args* a, fa_stream_t stream) {
   p.x_t = a->x_t;
   p.stage_cycles = a->stage_cycles;
   p.ws = static_cast<unsigned char*>(a->workspace);
-  p.L = layout(a->batch, a->Tv, a->Lkmax, sm ? 32 : 128, sm ? 64 : 128);
+  p.L = layout_for(a->batch, a->Tv, a->Lkmax);
   if (sm && (uint32_t)p.L.ntiles > kWsMaxCounters)
     return host::fail(FA_ERR_UNSUPPORTED, "fa_ma2_flow: %d fixup tiles exceed %u counters", p.L.ntiles, kWsMaxCounters);
   p.NL = a->num_layers;

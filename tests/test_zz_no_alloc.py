@@ -68,6 +68,49 @@ def test_noalloc_matches_workspace_entry_point(gpu):
     assert seen[0] == seen[1], "one scratch per device"
 
 
+def test_noalloc_on_fp16_caches(gpu):
+    """The reference's cache type at batch 1 (cache_dtype F16): no shadow is needed, so the entry point
+    that allocates nothing serves it; output and suffix cache rows equal fa_pi05_denoise's on copies of
+    the same fp16 caches (two calls, the second smaller)."""
+    L = _lib.lib()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    for NL, Lp, Tv, S, seed in ((2, 968, 50, 2, 61), (1, 200, 10, 2, 62)):
+        c = P.make_case(NL=NL, Lp=Lp, Tv=Tv, S=S, seed=seed)
+        g = P.gpu_tensors(c, gpu)
+        kb, vb = g["caches"][0]
+        runs = []
+        for noalloc in (True, False):
+            kh, vh = kb.to(torch.float16).contiguous(), vb.to(torch.float16).contiguous()
+            x_t = c["inp"]["noise"][0].to(gpu).clone()
+            a = _args(c, g, x_t)
+            a.kcache, a.vtcache = kh.data_ptr(), vh.data_ptr()
+            a.cache_dtype = _lib.FA_DTYPE_F16
+            if noalloc:
+                scratch = ctypes.c_void_p(0)
+                _lib.check(L.fa_pi05_denoise_noalloc(ctypes.byref(a), ctypes.c_void_p(stream), ctypes.byref(scratch)),
+                           "fa_pi05_denoise_noalloc")
+            else:
+                ws = pi05.workspace(gpu)
+                a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+                _lib.check(L.fa_pi05_denoise(ctypes.byref(a), ctypes.c_void_p(stream)), "fa_pi05_denoise")
+            torch.cuda.synchronize(gpu)
+            if noalloc:
+                st = ctypes.c_uint(7)
+                _lib.check(L.fa_pi05_read_status(scratch, ctypes.byref(st)), "fa_pi05_read_status")
+                assert st.value == 0
+            runs.append((x_t.cpu().numpy(), kh.cpu(), vh.cpu()))
+        (o1, k1, v1), (o2, k2, v2) = runs
+        st = P.parity(o1[:Tv], o2[:Tv])
+        print(f"noalloc vs fa_pi05_denoise on fp16 caches NL={NL} Lp={Lp} Tv={Tv} S={S}: {st}", flush=True)
+        assert np.isfinite(o1).all()
+        assert st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS, st
+        assert torch.equal(k1[:, :Lp], k2[:, :Lp]) and torch.equal(v1[:, :, :Lp], v2[:, :, :Lp])
+        for a1, a2 in ((k1[:, Lp:Lp + Tv].float(), k2[:, Lp:Lp + Tv].float()),
+                       (v1[:, :, Lp:Lp + Tv].float(), v2[:, :, Lp:Lp + Tv].float())):
+            assert torch.count_nonzero(a1) == a1.numel()
+            assert float((a1 - a2).abs().max()) <= 0.02 * float(a2.abs().max()) + 1e-3
+
+
 def test_noalloc_rejects_requests_beyond_its_scratch(gpu):
     L = _lib.lib()
     c = P.make_case(NL=1, Lp=50, Tv=50, S=1, seed=1)

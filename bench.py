@@ -1,4 +1,4 @@
-"""Benchmark: pi0.5 flow-matching denoise loop on one MI355X.
+"""Benchmark: pi0.5 flow-matching denoise loop on one MI355X (the batch-1 benchmark workload).
 
 One "step" = one full action chunk: the 10-step Euler loop of the 18-layer pi0.5 expert over a
 968-token prefix KV cache for 50 action tokens, bf16 operands / fp32 accumulation, batch 1,
@@ -7,10 +7,10 @@ as ONE cooperative kernel launch. Inputs are seeded synthetic tensors already re
 Prints one JSON line: value = ms per chunk (lower is better), the roofline of the kernel
 (algorithmic bytes / measured launch time vs 8 TB/s), the CPU fp32 oracle timed on the host
 cores (cpu_baseline), the parity of the first GPU chunk vs that oracle run, and "bs16": the
-metric's second half, chunks/s of the batch-16 launch and its MFMA
+metric's second half (the batch-16 workload), chunks/s of the batch-16 launch and its MFMA
 utilisation (algorithmic FLOPs / launch time vs 2.5 PFLOP/s dense bf16); "config3": the
 Gemma-2B-shaped prefix prefill that writes the K/V cache (ms, MFMA utilisation) and the prefill +
-denoise chain; "molmoact2": BASELINE config 4 at batch 1 (ms per chunk, HBM
+denoise chain (the benchmark's prefill workload); "molmoact2": the MolmoAct2 benchmark workload at batch 1 (ms per chunk, HBM
 roofline fraction, parity vs the CPU oracle) and batch 16.
 """
 from __future__ import annotations
@@ -104,7 +104,7 @@ def flops_per_launch(batch, nl=NL, lp=LP, tv=TV, s=S) -> int:
 
 
 def bench_batched(dev, batch, steps, warmup, seed=0, check=True):
-    """the batched launch (batch samples, each with its own prefix KV and noise).
+    """The batch-16 workload: the batched launch (batch samples, each with its own prefix KV and noise).
     With ``check``, samples 0 and batch-1 of the first launch are compared with the CPU oracle after
     the timed region (batch independence is covered by the tests)."""
     w = synthetic.pi05_weights(seed, dev, NL=NL)
@@ -190,7 +190,7 @@ def ma2_flops_per_launch(batch=1, c=MA2) -> int:
 
 
 def bench_ma2(dev, batch, launches, warmup=2, cpu=False, seed=0):
-    """MolmoAct2 expert, synthetic N(0, 0.02) weights and mods, N(0, 1) context."""
+    """The MolmoAct2 workload: MolmoAct2 expert, synthetic N(0, 0.02) weights and mods, N(0, 1) context."""
     from flashact_amd import ma2
     c = MA2
     w = synthetic.ma2_weights(seed, dev, NL=c["NL"], S=c["S"])
@@ -272,7 +272,7 @@ def prefill_flops(nl=NL, lp=LP) -> int:
 
 
 def bench_prefill(dev, launches, step_fn, kc, vc, seed=5, check=None):
-    """Gemma-2B-shaped prefill of a 968-token N(0, 1) prefix (18 layers) writing the
+    """The benchmark prefill workload: Gemma-2B-shaped prefill of a 968-token N(0, 1) prefix (18 layers) writing the
     expert's K/V cache, then the bs=1 denoise loop reading it. Times the prefill alone and the chain.
     ``check`` = (reset, output, oracle inputs of the denoise) runs one more chain after the timed region
     and compares its actions with the CPU oracle chain (oracle prefill -> bf16 K/V -> oracle loop)."""
@@ -395,15 +395,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline and parity check")
     ap.add_argument("--bs16-launches", type=int, default=10,
-                    help="timed launches of the batch-16 kernel (BASELINE config 2); 0 skips it")
+                    help="timed launches of the batch-16 kernel (the batch-16 workload); 0 skips it")
     ap.add_argument("--ma2-launches", type=int, default=10,
-                    help="timed launches of the MolmoAct2 kernel at batch 1 and 16 (BASELINE config 4); 0 skips")
+                    help="timed launches of the MolmoAct2 kernel at batch 1 and 16 (the MolmoAct2 workload); 0 skips")
     ap.add_argument("--ref-shape-launches", type=int, default=20,
                     help="timed bs=1 launches at the reference's published shape (Tv=10); 0 skips")
     ap.add_argument("--fp8-launches", type=int, default=20,
                     help="timed bs=1 launches with FP8-W8A16 weights (Tv=50 and Tv=10); 0 skips")
     ap.add_argument("--prefill-launches", type=int, default=10,
-                    help="timed prefill launches and prefill + denoise chains (BASELINE config 3); 0 skips")
+                    help="timed prefill launches and prefill + denoise chains (the benchmark's prefill workload); 0 skips")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="first run a plain device copy of this many bytes (twice), the calibration dispatch for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
@@ -421,7 +421,7 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    log("building the BASELINE config 1 inputs")
+    log("building the batch-1 benchmark inputs")
     w, inp, mods, modf, packed, cos, sin, Lmax, kc, vc = build_inputs(dev)
     x_t = inp["noise"][0].clone()
     empty = torch.empty(0, device=dev)
@@ -513,7 +513,7 @@ def main():
                                                                "prefix, 10 steps (src/pi05/README.md:19)"}
     if args.fp8_launches > 0:
         log("fp8 weights")
-        # FP8-W8A16 weights (the reference's pi0.5 numerics): BASELINE shape and the reference's Tv = 10.
+        # FP8-W8A16 weights (the reference's pi0.5 numerics): the benchmark shape and the reference's Tv = 10.
         pk8 = pi05.pack_weights_fp8(w["wq"], w["wk"], w["wv"], w["wo"], w["wg"], w["wu"], w["wd"])
         fp8 = {"workload": "pi05_expert_bs1_T50_Lp968_S10 with FP8-W8A16 weights (per-row e4m3)"}
         for tv_, key in ((TV, "T50"), (10, "T10")):

@@ -1,4 +1,4 @@
-// MolmoAct2 flow loop at batch 1 (Tv = 30 action tokens, Lk = 493 context
+// MolmoAct2 flow loop at batch 1 (the MolmoAct2 workload: Tv = 30 action tokens, Lk = 493 context
 // keys): the latency-bound case, laid out on the XCDs like the pi0.5 batch-1 kernel.
 //
 // One cooperative launch of 256 workgroups x 4 waves. XCD g = blockIdx % 8 owns attention head g;

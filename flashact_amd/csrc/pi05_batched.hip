@@ -1,4 +1,4 @@
-// pi0.5 action-expert denoise loop for a batch of samples (batch 16, M = 800
+// pi0.5 action-expert denoise loop for a batch of samples (the batch-16 workload: batch 16, M = 800
 // action tokens per GEMM): the whole S-step Euler loop in ONE cooperative launch of 256
 // workgroups x 4 waves, built on the stage engine (engine.h). This is the MFMA-bound regime, so
 // the GEMMs are 128-token tiles over all samples at once.

@@ -1,4 +1,4 @@
-// pi0.5 prefix prefill: the Gemma-2B-shaped backbone (D = 2048, 8 query heads /
+// pi0.5 prefix prefill (the benchmark's prefill workload): the Gemma-2B-shaped backbone (D = 2048, 8 query heads /
 // 1 K/V head of 256, F = 16384) over the Lp prefix tokens of each sample, in ONE cooperative launch
 // of 256 workgroups x 8 waves on the stage engine (engine.h). Its product is the K/V cache the
 // denoise loop reads: the QKV epilogue writes the RoPE'd keys into kcache rows [0, Lp) and the

@@ -13,8 +13,8 @@ from __future__ import annotations
 import torch
 
 PI05 = dict(NL=18, D=1024, H=8, HD=256, F=4096, AD=32)
-PI05_BASELINE = dict(Lp=968, Tv=50, S=10)
-BACKBONE = dict(NL=18, D=2048, H=8, HD=256, F=16384)  # BASELINE config 3 (Gemma-2B shape)
+PI05_BASELINE = dict(Lp=968, Tv=50, S=10)  # the pi0.5 expert workloads (batch 1 and 16)
+BACKBONE = dict(NL=18, D=2048, H=8, HD=256, F=16384)  # the prefix prefill workload (Gemma-2B shape)
 MA2 = dict(NL=36, D=768, H=8, HD=96, F=3072, AD=32)
 MA2_BASELINE = dict(Lk=493, Tv=30, S=10, adim=6)
 

@@ -232,7 +232,7 @@ int fa_ma2_read_status(const void* workspace, unsigned* status);
 int fa_ma2_max_batch(void);
 
 /* ---------------------------------------------------------------- pi0.5 prefix prefill
- * The Gemma-2B-shaped backbone over the prefix: D=2048, 8 query heads / 1 KV
+ * The Gemma-2B-shaped backbone over the prefix (the benchmark's prefill workload): D=2048, 8 query heads / 1 KV
  * head of 256, F=16384 GeLU-tanh-gated MLP, RMSNorm (eps 1e-6) scaled by (1 + w), RoPE (base
  * 10000, split-half pairs j, j+128) at positions 0..Lp-1, bidirectional attention over the prefix.
  * Replaces the reference's prefix prefill, openpi's PaliGemma forward with use_cache

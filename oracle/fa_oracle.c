@@ -31,7 +31,7 @@
  *
  * Weights use the reference's natural (unpacked) layouts, [out][in] row-major, stored as
  * bf16 bit patterns (uint16). Every value is converted exactly to fp32 and all arithmetic
- * is fp32, so the oracle and the GPU path see identical inputs and
+ * is fp32 (the CPU reference workload), so the oracle and the GPU path see identical inputs and
  * differ only in arithmetic precision. Pins: see tests/test_oracle_*.py.
  */
 #include <math.h>
@@ -574,7 +574,7 @@ int fo_ma2_flow(const fo_ma2_dims* dm, const uint16_t* w_qkv, const float* b_qkv
 }
 
 /* ------------------------------------------------------------------ */
-/* Gemma backbone prefix prefill                   */
+/* Gemma backbone prefix prefill (the benchmark's prefill workload)   */
 /* ------------------------------------------------------------------ */
 typedef struct {
   int NL, D, H, HD, F, Lp, batch;

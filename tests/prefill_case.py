@@ -1,4 +1,4 @@
-"""Seeded backbone-prefill cases (BASELINE config 3 shape) for the oracle (CPU) and the C ABI (GPU)."""
+"""Seeded backbone-prefill cases (the benchmark prefill shape) for the oracle (CPU) and the C ABI (GPU)."""
 from __future__ import annotations
 
 import numpy as np

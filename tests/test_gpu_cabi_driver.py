@@ -2,7 +2,7 @@
 ``flashact_amd.build``): no Python binding and no torch between the caller and the kernels.
 
 The test writes a seeded case as raw files, runs the driver as a child process, and compares the
-x_t it writes back with the CPU oracle at the BASELINE tolerance (max-abs <= 2e-2, mean-abs <= 2e-3);
+x_t it writes back with the CPU oracle at the acceptance tolerance (max-abs <= 2e-2, mean-abs <= 2e-3);
 for pi0.5 it also checks the suffix cache rows against a launch of the same case through ctypes.
 """
 import os

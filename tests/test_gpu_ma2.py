@@ -1,6 +1,6 @@
 """MolmoAct2 flow loop on the MI355X vs the CPU fp32 oracle (parity gate).
 
-Tolerance (bf16 operands with fp32 accumulation vs the fp32 oracle, on the
+Tolerance (the acceptance tolerance for bf16 operands with fp32 accumulation vs the fp32 oracle, on the
 final actions, integrated dims [0, adim)): max-abs <= 2e-2 and mean-abs <= 2e-3.
 """
 import numpy as np
@@ -34,7 +34,7 @@ def test_ma2_small(gpu):
 
 
 def test_ma2_config4_bs1(gpu):
-    """BASELINE config 4 at batch 1: 36 layers, Lk=493, Tv=30, adim=6, 10 steps."""
+    """The MolmoAct2 benchmark workload at batch 1: 36 layers, Lk=493, Tv=30, adim=6, 10 steps."""
     _check(C.make_case(NL=36, Lk=493, Tv=30, S=10), gpu)
 
 
@@ -48,7 +48,7 @@ def test_ma2_edge_shapes(gpu, B, Lk, Tv, S, adim):
 
 
 def test_ma2_batch16(gpu):
-    """BASELINE config 4 at batch 16 (the large-tile path) at full depth, 36 layers x 10 steps, every
+    """The MolmoAct2 benchmark workload at batch 16 (the large-tile path) at full depth, 36 layers x 10 steps, every
     sample against the oracle (benchmarks/molmoact2/eval_numerics.py:147-159 is the reference's
     fidelity check of the same loop)."""
     _check(C.make_case(NL=36, Lk=493, Tv=30, S=10, batch=16), gpu)

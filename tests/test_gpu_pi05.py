@@ -1,6 +1,6 @@
 """pi0.5 denoise loop on the MI355X vs the CPU fp32 oracle (parity gate).
 
-Tolerance (bf16 operands with fp32 accumulation vs the fp32 oracle, on
+Tolerance (the acceptance tolerance for bf16 operands with fp32 accumulation vs the fp32 oracle, on
 the final actions): max-abs <= 2e-2 and mean-abs <= 2e-3.
 """
 import numpy as np
@@ -32,7 +32,7 @@ def test_pi05_small_two_layers(gpu):
 
 
 def test_pi05_full_baseline_shape(gpu):
-    """BASELINE config 1 vs config 0: 18 layers, Lp=968, Tv=50, 10 steps."""
+    """The batch-1 benchmark workload vs the fp32 oracle: 18 layers, Lp=968, Tv=50, 10 steps."""
     _check(P.make_case(NL=18, Lp=968, Tv=50, S=10), gpu)
 
 

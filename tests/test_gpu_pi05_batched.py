@@ -1,6 +1,6 @@
 """Batched pi0.5 denoise loop (batch >= 2: the MFMA-bound kernel) on the MI355X vs the CPU fp32 oracle.
 
-Tolerance (bf16 operands with fp32 accumulation vs the fp32 oracle, on the
+Tolerance (the acceptance tolerance for bf16 operands with fp32 accumulation vs the fp32 oracle, on the
 final actions of every sample): max-abs <= 2e-2 and mean-abs <= 2e-3.
 """
 import numpy as np
@@ -41,7 +41,7 @@ def test_batched_edge_shapes(gpu, B, Lp, Tv, S):
 
 
 def test_batched_baseline_config2(gpu):
-    """BASELINE config 2 vs config 0: batch 16, 18 layers, Lp=968, Tv=50, 10 steps."""
+    """The batch-16 benchmark workload vs the fp32 oracle: batch 16, 18 layers, Lp=968, Tv=50, 10 steps."""
     _check(P.make_case(NL=18, Lp=968, Tv=50, S=10, batch=16), gpu)
 
 

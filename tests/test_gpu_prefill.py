@@ -1,11 +1,11 @@
-"""pi0.5 prefix prefill on the MI355X vs the CPU fp32 oracle.
+"""pi0.5 prefix prefill (the benchmark's prefill workload) on the MI355X vs the CPU fp32 oracle.
 
 Two gates:
   * the K/V cache the prefill writes (bf16) against the oracle's fp32 K/V of every layer:
     max-abs <= 4e-2 and mean-abs <= 4e-3 (K and V have unit scale here; a bf16 output alone is
     off by up to 2^-9 relative, and bf16 GEMM operands through the layers add about as much again);
   * end to end (prefill, then the 10-step-style denoise loop reading that cache) against the
-    oracle chain, on the final actions, with the BASELINE tolerance: max-abs <= 2e-2 and
+    oracle chain, on the final actions, with the acceptance tolerance: max-abs <= 2e-2 and
     mean-abs <= 2e-3. The oracle chain casts its fp32 K/V to bf16 between the two stages, as the
     reference's hand-off does (src/pi05/pack_weights.py:70).
 """
@@ -53,7 +53,7 @@ def test_prefill_edge_shapes(gpu, Lp, B):
 
 @pytest.fixture(scope="module")
 def config3(gpu):
-    """BASELINE config 3's prefill (18 layers, Lp = 968) on the GPU and in the oracle, shared by the
+    """The benchmark's prefill (18 layers, Lp = 968) on the GPU and in the oracle, shared by the
     full-depth K/V check and the full chain below (the oracle prefill is the slow part)."""
     c = C.make_case(NL=18, Lp=968)
     Lmax = pi05.lmax_for(968, 50)
@@ -65,7 +65,7 @@ def config3(gpu):
 
 
 def test_prefill_config3_all_layers(config3):
-    """The full BASELINE config 3 launch: K/V of every one of the 18 layers against the oracle.
+    """The full benchmark prefill launch: K/V of every one of the 18 layers against the oracle.
 
     Through 18 layers of a 2048-wide residual stream the bf16 roundings compound: the error to the
     fp32 oracle grows from 1.7e-3 (layer 0) to about 8.7e-3 mean-abs (layer 17) for K and V of unit
@@ -91,7 +91,7 @@ def test_prefill_config3_all_layers(config3):
 
 
 def test_config3_full_chain(gpu, config3):
-    """BASELINE config 3 end to end at full size: the 18-layer prefill over 968 tokens writes the
+    """The benchmark prefill end to end at full size: the 18-layer prefill over 968 tokens writes the
     caches, the 18-layer, 10-step, Tv = 50 denoise loop reads them; final actions against the oracle
     chain (oracle prefill -> bf16 K/V -> oracle denoise), as eval_numerics.py:50-69 and :81-107 chain
     openpi's prefill, the cache fill and the loop."""

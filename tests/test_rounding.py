@@ -5,7 +5,7 @@ operands, chunked attention, fp16 partial sums with the parity bit). Run once wi
 exchanged exactly and once as the kernel exchanges them, the two distances to the fp32 oracle isolate
 the exchange's share. On the hardest case (18 layers, one Euler step of dt = -1, every residual gate 1,
 all 32 action dims integrated) the fp16 exchange adds 3.8 % to the error of the bf16 operands alone
-(mean-abs 6.46e-3 -> 6.70e-3); 2.5 % on the BASELINE shape (3.09e-4 -> 3.16e-4). The reference keeps
+(mean-abs 6.46e-3 -> 6.70e-3); 2.5 % on the benchmark shape (18 layers x 10 steps, Lp = 968, Tv = 50) (3.09e-4 -> 3.16e-4). The reference keeps
 the partial sums in fp32 (src/pi05/mk6.cu:63, 147). The restatement's own planted mistake (a dropped
 exchange rounding would leave the two runs equal) is ruled out by requiring them to differ.
 """

@@ -2,7 +2,7 @@
 
 Both run the same kernels; the no-allocation one on the library's static device scratch instead of
 a caller workspace. Two calls in a row (the second with a smaller input: fewer prefix keys, fewer
-action tokens), each compared with fa_pi05_denoise on the same inputs at the BASELINE tolerance
+action tokens), each compared with fa_pi05_denoise on the same inputs at the acceptance tolerance
 (max-abs <= 2e-2, mean-abs <= 2e-3; in practice the two agree to a few ulp, the exchange parity
 bit of each workspace's launch history being the only difference), plus the kernel status read
 from the scratch address the call reports, and the size limit.

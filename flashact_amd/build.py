@@ -19,6 +19,8 @@ DRIVER_PATH = os.path.join(ROOT, "tests", "bin", "cabi_driver")
 # litmus tests of the cross-CU / cross-XCD message passing the kernels rely on (tests/litmus_xcd.hip)
 LITMUS_SRC = os.path.join(ROOT, "tests", "litmus_xcd.hip")
 LITMUS_PATH = os.path.join(ROOT, "tests", "bin", "litmus_xcd")
+FABRIC_SRC = os.path.join(ROOT, "tests", "fabric_probe.hip")
+FABRIC_PATH = os.path.join(ROOT, "tests", "bin", "fabric_probe")
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -125,6 +127,7 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB_PATH)
     build_driver(hipcc)
     build_litmus(hipcc)
+    build_probe(hipcc, FABRIC_SRC, FABRIC_PATH)
     return LIB_PATH
 
 
@@ -144,14 +147,19 @@ def build_driver(hipcc: str) -> str:
 
 
 def build_litmus(hipcc: str) -> str:
-    os.makedirs(os.path.dirname(LITMUS_PATH), exist_ok=True)
-    tmp = LITMUS_PATH + ".tmp"
-    cmd = [hipcc, *HIPCC_FLAGS, LITMUS_SRC, "-o", tmp]
+    return build_probe(hipcc, LITMUS_SRC, LITMUS_PATH)
+
+
+def build_probe(hipcc: str, src: str, path: str) -> str:
+    """A standalone test program (one .hip file, no library) -> tests/bin."""
+    os.makedirs(os.path.dirname(path), exist_ok=True)
+    tmp = path + ".tmp"
+    cmd = [hipcc, *HIPCC_FLAGS, src, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {LITMUS_SRC} ({res.returncode}):\n{res.stdout}{res.stderr}")
-    os.replace(tmp, LITMUS_PATH)
-    return LITMUS_PATH
+        raise RuntimeError(f"hipcc failed on {src} ({res.returncode}):\n{res.stdout}{res.stderr}")
+    os.replace(tmp, path)
+    return path
 
 
 if __name__ == "__main__":

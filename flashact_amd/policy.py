@@ -1,4 +1,6 @@
-"""pi0.5 policy wrapper: checkpoint loading and a ``predict`` call over the MI355X kernels.
+"""Policy wrappers: checkpoint loading and a ``predict`` call over the MI355X kernels.
+
+``Pi05Policy`` (pi0.5) and ``Ma2Policy`` (MolmoAct2, at the end of this file).
 
 Mirrors the reference's ``HybridPi05`` (src/pi05/hybrid_model.py:23-228) minus its FlashRT
 front-end (vision encoder, tokenizer, encoder CUDA graph), which is outside this build:
@@ -27,7 +29,7 @@ import re
 import numpy as np
 import torch
 
-from . import pi05, prefill
+from . import ma2, pi05, prefill
 
 EXPERT = "paligemma_with_expert.gemma_expert.model."
 D, HD, F, AD = 1024, 256, 4096, 32
@@ -185,4 +187,114 @@ class Pi05Policy:
         pi05.launch(p["w1"], p["wo"], p["w2"], p["w3"], *sc, self.mods, self.mod_final,
                     cos, sin, self.w_ain, self.b_ain, self.w_aout, self.b_aout, ksrc, vsrc, srows, kc, vc, Lp, Lmax,
                     self.num_steps, self.chunk_size, x_t, check_status=True)
+        return x_t.cpu().numpy()
+
+
+# ---------------------------------------------------------------- MolmoAct2
+MA2_LAYER = "blocks.0.self_attn.qkv.weight"
+
+
+def find_ma2_prefix(src) -> str | None:
+    """The action expert's prefix P in a MolmoAct2 state dict: P + 'blocks.0.self_attn.qkv.weight'."""
+    for k in sorted(src.keys()):
+        if k.endswith(MA2_LAYER):
+            return k[: -len(MA2_LAYER)]
+    return None
+
+
+class Ma2Policy:
+    """MolmoAct2 action-expert weights resident on one GPU, ready for ``predict``.
+
+    Mirrors the reference's MolmoAct2 harness (benchmarks/molmoact2/eval_numerics.py:77-133,
+    eval_e2e.py:81-144) without the HF model around the expert:
+      * the weights are read by module name from a state dict or ``.safetensors`` file, under the expert's
+        prefix P (found as the P with P + 'blocks.0.self_attn.qkv.weight', or given): per layer l
+        ``blocks.l.self_attn.qkv`` [2304][768], ``self_attn.out_proj``, ``cross_attn.q_proj``,
+        ``cross_attn.out_proj`` [768][768], ``mlp.gate_proj`` / ``mlp.up_proj`` [3072][768],
+        ``mlp.down_proj`` [768][3072] (weights and biases), then ``action_embed`` [768][32] and
+        ``final_layer.linear`` [32][768]; gate/up rows and biases are interleaved as the reference packs
+        them (eval_numerics.py:88-93);
+      * the per-step modulations, the encoder context and the RoPE base come from the HF model's
+        ``prepare_modulation_cache``, ``prepare_context`` and rotary module in the reference; ``predict``
+        takes them as inputs, in the reference's packed layouts.
+    There is no fallback: every call runs the HIP kernels through the C ABI.
+    """
+
+    def __init__(self, checkpoint, *, expert_prefix: str | None = None, num_steps: int = 10, chunk_size: int = 30,
+                 action_dims: int = 6, device="cuda"):
+        if not 1 <= chunk_size <= ma2.MAX_TV:
+            raise ValueError(f"chunk_size must be in [1, {ma2.MAX_TV}], got {chunk_size}")
+        if not 0 <= action_dims <= AD:
+            raise ValueError(f"action_dims must be in [0, {AD}], got {action_dims}")
+        self.num_steps, self.chunk_size, self.adim = int(num_steps), int(chunk_size), int(action_dims)
+        self.device = torch.device(device)
+        src = _Source(checkpoint)
+        P = expert_prefix if expert_prefix is not None else find_ma2_prefix(src)
+        if P is None or P + MA2_LAYER not in src:
+            raise KeyError(f"no MolmoAct2 expert layers ('...{MA2_LAYER}') in the checkpoint")
+        pat = re.compile(re.escape(P) + r"blocks\.(\d+)\.self_attn\.qkv\.weight$")
+        self.num_layers = max(int(m.group(1)) for k in src.keys() for m in [pat.match(k)] if m) + 1
+        dev, NL = self.device, self.num_layers
+
+        def st(name, shape):
+            ts = []
+            for l in range(NL):
+                key = f"{P}blocks.{l}.{name}"
+                t = src[key]
+                if tuple(t.shape) != shape:
+                    raise ValueError(f"{key}: shape {tuple(t.shape)}, expected {shape}")
+                ts.append(t.to(dev))
+            return torch.stack(ts)
+
+        D, FF = ma2.D, ma2.FF
+        proj = (("self_attn.qkv", 3 * D, D), ("self_attn.out_proj", D, D), ("cross_attn.q_proj", D, D),
+                ("cross_attn.out_proj", D, D), ("mlp.gate_proj", FF, D), ("mlp.up_proj", FF, D),
+                ("mlp.down_proj", D, FF))
+        w = [st(n + ".weight", (o, i)) for n, o, i in proj]
+        b = [st(n + ".bias", (o,)) for n, o, i in proj]
+        self.ws, self.bs = ma2.pack_weights(*w, *b)
+        f = lambda k: src[P + k].float().to(dev).contiguous()  # noqa: E731
+        self.w_ain, self.b_ain = f("action_embed.weight"), f("action_embed.bias")
+        self.w_aout = src[P + "final_layer.linear.weight"].to(dev).to(torch.bfloat16).contiguous()
+        self.b_aout = f("final_layer.linear.bias")
+        if tuple(self.w_ain.shape) != (ma2.D, AD) or tuple(self.w_aout.shape) != (AD, ma2.D):
+            raise ValueError(f"action_embed {tuple(self.w_ain.shape)} / final_layer.linear {tuple(self.w_aout.shape)}: "
+                             f"expected ({ma2.D}, {AD}) / ({AD}, {ma2.D})")
+
+    def initial_noise(self, generator=None) -> torch.Tensor:
+        """N(0, 1) [chunk_size][32] with the dims past action_dims zeroed (eval_numerics.py:62-65)."""
+        x = torch.zeros(self.chunk_size, AD, dtype=torch.float32, device=self.device)
+        x.normal_(generator=generator)
+        x[:, self.adim:] = 0
+        return x
+
+    def predict(self, kv_contexts, mods, mod_final, *, cross_mask=None, rope=None, noise=None,
+                generator=None) -> np.ndarray:
+        """One action chunk [chunk_size][32] (fp32; dims past action_dims stay as the noise left them, 0).
+
+        kv_contexts: per layer (k, v), each [1][L][8][96] or [1][L][768] (the encoder's context, as
+        ``prepare_context`` gives it), compacted to the rows ``cross_mask`` keeps (``ma2.compact_context``);
+        mods [num_steps][NL][3][3][768] fp32: (scale, shift, gate) of the self-attention, cross-attention
+        and MLP norms; mod_final [num_steps][2][768]: (scale, shift) of the final norm
+        (eval_numerics.py:97-110); rope: (cos, sin) [chunk_size][48], default ``ma2.rope_table`` (base
+        10000; the model's rotary module sets it); noise [chunk_size][32], default ``initial_noise``.
+        """
+        dev, NL, S, Tv = self.device, self.num_layers, self.num_steps, self.chunk_size
+        if len(kv_contexts) != NL:
+            raise ValueError(f"kv_contexts has {len(kv_contexts)} layers, the expert {NL}")
+        mods = mods.to(dev, torch.float32).contiguous()
+        mod_final = mod_final.to(dev, torch.float32).contiguous()
+        if tuple(mods.shape) != (S, NL, 3, 3, ma2.D) or tuple(mod_final.shape) != (S, 2, ma2.D):
+            raise ValueError(f"mods {tuple(mods.shape)} / mod_final {tuple(mod_final.shape)}: expected "
+                             f"{(S, NL, 3, 3, ma2.D)} / {(S, 2, ma2.D)}")
+        kctx, vtctx, Lk = ma2.compact_context([(k.to(dev), v.to(dev)) for k, v in kv_contexts], cross_mask)
+        cos, sin = rope if rope is not None else ma2.rope_table(Tv, device=dev)
+        cos, sin = cos.to(dev, torch.float32).contiguous(), sin.to(dev, torch.float32).contiguous()
+        x_t = noise.to(dev, torch.float32).clone() if noise is not None else self.initial_noise(generator)
+        if tuple(x_t.shape) != (Tv, AD):
+            raise ValueError(f"noise {tuple(x_t.shape)}: expected {(Tv, AD)}")
+        # check_status: waits for the chunk and raises (after re-initialising the workspace) on a capped
+        # wait or an unexpected XCD placement, so an invalid chunk is never returned
+        ma2.launch(self.ws, self.bs, mods, mod_final, cos, sin, self.w_ain, self.b_ain, self.w_aout, self.b_aout,
+                   kctx, vtctx, Lk, int(kctx.shape[1]), Tv, self.adim, S, x_t, check_status=True)
         return x_t.cpu().numpy()

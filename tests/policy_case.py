@@ -48,3 +48,25 @@ def checkpoint(NL=2, seed=0, device="cpu", backbone=False, std=0.02):
             sd[p + "input_layernorm.weight"] = n(2048)
             sd[p + "post_attention_layernorm.weight"] = n(2048)
     return sd
+
+
+MA2_EXPERT = "model.action_expert."  # any prefix: Ma2Policy finds it by the first block's qkv key
+
+
+def ma2_checkpoint(c, prefix=MA2_EXPERT):
+    """A MolmoAct2 expert state dict with the module names the reference packs from
+    (benchmarks/molmoact2/eval_numerics.py:78-118), holding the weights of ma2_case.make_case ``c``."""
+    w = c["w"]
+    sd = {}
+    for l in range(c["NL"]):
+        b = f"{prefix}blocks.{l}."
+        for name, key in (("self_attn.qkv", "qkv"), ("self_attn.out_proj", "so"), ("cross_attn.q_proj", "cq"),
+                          ("cross_attn.out_proj", "co"), ("mlp.gate_proj", "g"), ("mlp.up_proj", "u"),
+                          ("mlp.down_proj", "dn")):
+            sd[b + name + ".weight"] = w["w_" + key][l].clone()
+            sd[b + name + ".bias"] = w["b_" + key][l].clone()
+    sd[prefix + "action_embed.weight"] = w["w_ain"].clone()
+    sd[prefix + "action_embed.bias"] = w["b_ain"].clone()
+    sd[prefix + "final_layer.linear.weight"] = w["w_aout"].clone()
+    sd[prefix + "final_layer.linear.bias"] = w["b_aout"].clone()
+    return sd

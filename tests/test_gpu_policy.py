@@ -112,3 +112,31 @@ def test_predict_fp8_weights(setup):
     print(f"policy fp8 path: {st}", flush=True)
     assert st["max_abs"] <= 2e-2 and st["mean_abs"] <= 2e-3, st
     assert not np.array_equal(out, pol.predict(x, noise=noise))  # the weights really are quantised
+
+
+def test_ma2_policy_predict(gpu):
+    """MolmoAct2: checkpoint (module names) -> Ma2Policy.predict -> the chunk, against the oracle on the
+    same weights; then with a boolean context mask, against the oracle on the rows the mask keeps."""
+    from tests import ma2_case as M
+    # 5 steps: with unit gates the bf16-operand error floor falls with the step size (1.4e-3 mean-abs
+    # at 2 steps, close to the 2e-3 tolerance)
+    c = M.make_case(NL=2, Lk=40, Tv=30, S=5, seed=9)
+    sd = {k: v.to(gpu) for k, v in PC.ma2_checkpoint(c).items()}
+    pol = policy.Ma2Policy(sd, num_steps=5, chunk_size=30, action_dims=c["adim"], device=gpu)
+    kv = [(c["inp"]["kctx"][0, l][None], c["inp"]["vctx"][0, l][None]) for l in range(2)]
+    out = pol.predict(kv, c["w"]["mods"], c["w"]["mod_final"], noise=c["inp"]["noise"][0])
+    st = M.parity(out, M.run_oracle(c)[0], c["adim"])
+    print(f"Ma2Policy.predict vs oracle: {st}", flush=True)
+    assert st["max_abs"] <= 2e-2 and st["mean_abs"] <= 2e-3, st
+    assert np.all(out[:, c["adim"]:] == 0)
+
+    keep = torch.ones(40, dtype=torch.bool)
+    keep[3::5] = False  # 8 of the 40 context rows masked out
+    out_m = pol.predict(kv, c["w"]["mods"], c["w"]["mod_final"], cross_mask=keep, noise=c["inp"]["noise"][0])
+    cm = dict(c)
+    cm["inp"] = dict(c["inp"], kctx=c["inp"]["kctx"][:, :, keep], vctx=c["inp"]["vctx"][:, :, keep])
+    cm["Lk"] = int(keep.sum())
+    st_m = M.parity(out_m, M.run_oracle(cm)[0], c["adim"])
+    print(f"Ma2Policy.predict with a context mask vs oracle on the kept rows: {st_m}", flush=True)
+    assert st_m["max_abs"] <= 2e-2 and st_m["mean_abs"] <= 2e-3, st_m
+    assert np.abs(out_m - out).max() > 0  # the mask changed the context

@@ -41,7 +41,7 @@ constexpr int MAX_LK = NR / 2 * KPR;
 
 // ---- workspace (bytes)
 constexpr uint32_t OFF_CTRL = 0;     // u64 seq, u32 err @8, u32 exchange parity bases @12, @16
-constexpr uint32_t OFF_XFLAG = 1024; // [8 XCD][32 rank] u64 epochs
+constexpr uint32_t OFF_XFLAG = 1024; // [8 XCD][32 rank][4 wave] u64 epochs
 constexpr uint32_t OFF_XP = kWsDataBase;  // [2 buffers][8 XCD][32 tokens][768] f32 (parity-tagged)
 constexpr uint32_t XP_BYTES = 2 * NX * TP * D * 4;
 // per-XCD block (stride XB): activations in MFMA fragment order and small fp32 intermediates.
@@ -59,7 +59,7 @@ constexpr uint32_t X_H = X_CML + 16 * TP * 8;         // [32][384] bf16 fragment
 constexpr uint32_t XB = (X_H + TP * 384 * 2 + 4095) / 4096 * 4096;
 constexpr uint32_t OFF_XCD = OFF_XP + XP_BYTES;
 constexpr uint32_t WS_BYTES = OFF_XCD + NX * XB;
-static_assert(OFF_XFLAG + NX * NR * 8 <= kWsCounters, "flags stay below the fixup counters");
+static_assert(OFF_XFLAG + NX * NR * 4 * 8 <= kWsCounters, "flags stay below the fixup counters");
 
 // ---- LDS
 constexpr uint32_t L_ATT = 0;                       // attention fragments (36 KB)
@@ -112,26 +112,29 @@ __device__ __forceinline__ bool aborted(const Ctx& c) {
   return __hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin;
 }
 
-// ---- XCD barrier (workgroup level): every wave drains its stores, rank r publishes its epoch to
-// its flag (same-XCD L2), then wave 0 polls the 32 flags of the XCD. Work that does not depend on
-// the barrier (weight prefetch) goes between arrive and wait.
-// XCD barrier: arrive publishes this workgroup's epoch with a plain store, which stays in the
-// XCD's L2 where the other 31 ranks' sc1 polls find it (a device-scope store went out to memory
-// and back: 15.8 -> 13.0 ms per chunk with the plain store). Only this XCD reads these flags; the
-// prologue's grid-wide barrier, read across XCDs, stores them device-scope.
+// ---- XCD barrier on per-wave epoch flags [XCD][rank][wave]. Work that does not depend on the
+// barrier (weight prefetch) goes between arrive and wait. The flags are plain stores, which stay in
+// the XCD's L2 where the other ranks' sc1 polls find them (a device-scope store went out to memory
+// and back: 15.8 -> 13.0 ms per chunk with the plain store); only this XCD reads them, and the
+// prologue's grid-wide barrier, read across XCDs, stores them device-scope. Every wave publishes its
+// own arrival and polls the XCD's 128 flags itself (one 16-byte sc1 load per lane), with no
+// workgroup barrier. A wave passes only after every wave of the XCD, its own
+// workgroup's included, has drained its global and LDS operations and published, so LDS written or
+// read before the barrier by a sibling wave is settled for all of them. Against one flag per
+// workgroup (a workgroup barrier, then wave 0 polling 32 flags while the others wait at a second
+// workgroup barrier): 11.48-11.55 -> 11.15-11.17 ms per chunk.
 __device__ __forceinline__ void xarrive(Ctx& c) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's global and LDS operations are complete
   c.e += 1;
-  if (threadIdx.x == 0) __hip_atomic_store(c.xflag + c.r, c.e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (c.lane == 0) __hip_atomic_store(c.xflag + c.r * 4 + c.w, c.e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 __device__ __forceinline__ void xwait(Ctx& c) {
-  if (c.w == 0 && !aborted(c)) {
-    const rsrc_t fr = make_rsrc(c.xflag, NR * 8);
+  if (!aborted(c)) {
+    const rsrc_t fr = make_rsrc(c.xflag, NR * 4 * 8);
     for (unsigned it = 0;; ++it) {
-      const u32x2 v = ldb64<kCpSc1>(fr, (uint32_t)(c.lane & 31) * 8);
-      const uint64_t f = ((uint64_t)v[1] << 32) | v[0];
-      if (__builtin_amdgcn_ballot_w64(f < c.e) == 0) break;
+      const u32x4 v = ldb128<kCpSc1>(fr, (uint32_t)c.lane * 16);
+      const uint64_t f0 = ((uint64_t)v[1] << 32) | v[0], f1 = ((uint64_t)v[3] << 32) | v[2];
+      if (__builtin_amdgcn_ballot_w64(f0 < c.e || f1 < c.e) == 0) break;
       if (it > kSpinCap) {
         if (c.lane == 0) atomicOr(c.err, kErrSpin);
         break;
@@ -139,7 +142,6 @@ __device__ __forceinline__ void xwait(Ctx& c) {
       __builtin_amdgcn_s_sleep(1);
     }
   }
-  __syncthreads();
   asm volatile("" ::: "memory");
 }
 
@@ -589,7 +591,7 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
   c.lq = c.lane >> 4;
   c.ws = rsrc_all(p.ws);
   c.xb = OFF_XCD + (uint32_t)c.g * XB;
-  c.xflag = reinterpret_cast<uint64_t*>(p.ws + OFF_XFLAG) + c.g * NR;
+  c.xflag = reinterpret_cast<uint64_t*>(p.ws + OFF_XFLAG) + c.g * NR * 4;
   c.err = reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 8);
   const uint64_t seq = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
   c.e = seq << 32;
@@ -609,8 +611,8 @@ __global__ void __launch_bounds__(NTHR, 1) ma2x_kernel(Params p) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     c.e += 1;
-    if (threadIdx.x == 0) __hip_atomic_store(c.xflag + c.r, c.e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (c.w == 0) poll_flags(c.ws, OFF_XFLAG, NX * NR * 8, c.e, c.err);
+    if (c.lane == 0) __hip_atomic_store(c.xflag + c.r * 4 + c.w, c.e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    poll_flags(c.ws, OFF_XFLAG, NX * NR * 4 * 8, c.e, c.err);
     __syncthreads();
   }
   float* xt = reinterpret_cast<float*>(lds + L_XT);

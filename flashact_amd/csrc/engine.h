@@ -127,10 +127,17 @@ struct Grid {
   uint64_t e;
 };
 
-__device__ __forceinline__ void grid_sync(Grid& g) {
+struct NoSide {
+  __device__ void operator()() const {}
+};
+// side(): run by waves 1.. while wave 0 waits at the barrier; work that needs nothing the barrier
+// publishes (copies of launch inputs into LDS, which is free once the first workgroup barrier passed)
+template <class F = NoSide>
+__device__ __forceinline__ void grid_sync(Grid& g, const F& side = F{}) {
   __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
   __syncthreads();
   g.e += 1;
+  if (threadIdx.x >= 64) side();
   const int x = blockIdx.x & 7, rk = blockIdx.x >> 3, lane = threadIdx.x & 63;
   // flag stores through a wave-uniform descriptor (a generic pointer would keep the 64-bit address in
   // VGPRs across the whole layer loop)

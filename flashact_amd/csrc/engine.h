@@ -198,7 +198,8 @@ __device__ __forceinline__ u32x4 pack_pre(const E& e, int n, f32x4 v, const type
 // rows r, r+16, r+32, r+48 (k step = 256 B each, 16 lanes per row) and lands them as 4 x 256 B at
 // LDS pitch 1040 B. An MFMA fragment (16 rows of one 16-row block, 32 k) then reads row r from
 // copy r at 1040 r + 256 (block % 4) + 64 ks + 16 q: the 16 rows fall in 16 different bank groups.
-// Two-step ring, one workgroup barrier per step. Rows m >= M copy row 0 (results discarded).
+// Ring of RD steps (2, or 3 where three fit the kernel's LDS: two steps then stay in flight while one
+// computes), one workgroup barrier per step. Rows m >= M copy row 0 (results discarded).
 // With AF the activations are in MFMA fragment order instead (fragment (token block tb, k-step kk) =
 // 1 KB at (tb lda / 32 + kk) * 1024, lane l = lr + 16 q holding token lr, k 8q..8q+7 at 16 l): copy f
 // of a step is fragment (token block f / 4, k-step f % 4), one contiguous 1 KB, and lands whole in slot
@@ -221,7 +222,7 @@ struct GemmShape {
   static_assert(BN % 64 == 0, "weight tiles are whole 64-row groups");
 };
 
-template <int WM, int WN, bool AF = false, class Epi>
+template <int WM, int WN, bool AF = false, int RD = 2, class Epi>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int k0, int k1, Epi& epi) {
   using S = GemmShape<WM, WN>;
   const int w = wave_id(), lane = lane_id(), lr = lane & 15, lq = lane >> 4;
@@ -253,7 +254,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
   }
   const int ns = (k1 - k0) >> 7;
   auto issue = [&](int s) {
-    const uint32_t base = (uint32_t)(s & 1) * S::STEP;
+    const uint32_t base = (uint32_t)(s % RD) * S::STEP;
 #pragma unroll
     for (int j = 0; j < S::IPW; j++) {
       const int f = w + NWAVE * j;
@@ -282,13 +283,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
       }
   }
   issue(0);
+  if (RD > 2 && ns > 1) issue(1);
 #pragma unroll 1
   for (int s = 0; s < ns; s++) {
-    vm_wait<0>();
+    if (RD > 2 && s + 1 < ns)
+      vm_wait<S::IPW>();  // step s + 1's copies (the last issued) may still be in flight
+    else
+      vm_wait<0>();
     __syncthreads();  // step s landed for every wave; every wave is done with step s - 1
-    if (s + 1 < ns) issue(s + 1);
+    if (s + RD - 1 < ns) issue(s + RD - 1);
     if (!cw) continue;
-    const uint32_t base = (uint32_t)(s & 1) * S::STEP;
+    const uint32_t base = (uint32_t)(s % RD) * S::STEP;
     // fragments of k sub-step ks + 1 are read while the MFMAs of ks run (double-buffered)
     u32x4 a[2][WM], b[2][WN];
     auto rd = [&](int ks, int h) {
@@ -395,7 +400,7 @@ struct NoPre {
 // Runs every tile of an [M x N] GEMM, K split into `ksplit` equal ranges (multiples of 128). Items
 // are ordered m-tile fastest so the items of one weight tile run on neighbouring CUs of one XCD.
 // The epilogue receives the split index through epi.split.
-template <int WM, int WN, bool AF = false, class Epi>
+template <int WM, int WN, bool AF = false, int RD = 2, class Epi>
 __device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int ksplit, Epi& epi) {
   using S = GemmShape<WM, WN>;
   const int nm = (g.M + S::BM - 1) / S::BM, nn = N / S::BN;
@@ -404,7 +409,7 @@ __device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int 
   for (int it = vwg(); it < items; it += NWG) {
     const int mt = it % nm, rest = it / nm, nt = rest % nn, sp = rest / nn;
     epi.split = sp;
-    gemm_tile<WM, WN, AF>(g, mt * S::BM, nt * S::BN, sp * kc, sp * kc + kc, epi);
+    gemm_tile<WM, WN, AF, RD>(g, mt * S::BM, nt * S::BN, sp * kc, sp * kc + kc, epi);
   }
 }
 

@@ -128,7 +128,7 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xt
   const rsrc_t rbi = make_rsrc(p.b_ain, D * 4), rwi = make_rsrc(p.w_ain, D * AD * 4);
   const rsrc_t rwo = make_rsrc(p.w_aout, AD * D * 4), rbo = make_rsrc(p.b_aout, AD * 4);
 #pragma unroll 1
-  for (int m = vwg() * 4 + wave_id(); m < L.M; m += nwave) {
+  for (int m = wave_id() * NWG + (int)blockIdx.x; m < L.M; m += nwave) {
     const int b = m / p.Tv, t = m - b * p.Tv;
     const uint32_t xto = (uint32_t)(((size_t)b * p.xt_rows + t) * AD * 4);
     f32x4 x[4];

@@ -400,13 +400,30 @@ struct NoPre {
 // Runs every tile of an [M x N] GEMM, K split into `ksplit` equal ranges (multiples of 128). Items
 // are ordered m-tile fastest so the items of one weight tile run on neighbouring CUs of one XCD.
 // The epilogue receives the split index through epi.split.
-template <int WM, int WN, bool AF = false, int RD = 2, class Epi>
+// This workgroup's first item of a stage whose items come in groups of gs consecutive items sharing a
+// weight tile. With at least NWG items: the XCD-major order vwg(). With fewer, XCD x takes the
+// contiguous run of groups [ng x / 8, ng (x + 1) / 8), so every XCD runs about items / 8 of them where
+// the XCD-major order fills XCDs 0, 1, .. and leaves the last ones idle; a group's items stay on one
+// XCD, whose L2 serves the weight tile's later reads, and neighbouring groups (the same k range)
+// share their activation tiles there too. Returns items for an idle workgroup; falls back to vwg()
+// when an XCD's run of groups would not fit its 32 workgroups.
+__device__ __forceinline__ int first_item(int items, int gs) {
+  const int ng = (items + gs - 1) / gs;
+  if (items >= NWG || (ng + 7) / 8 * gs > 32) return vwg();
+  const int x = blockIdx.x & 7, r = blockIdx.x >> 3;
+  const int it = ng * x / 8 * gs + r;
+  return it < min(ng * (x + 1) / 8 * gs, items) ? it : items;
+}
+
+// XB: items placed by first_item (batched MolmoAct2: 34.13 -> 33.34 ms per launch at batch 16); the
+// pi0.5 batched kernel (QKV 15.1 -> 15.5 us per layer) and the prefill (no change) keep vwg().
+template <int WM, int WN, bool AF = false, int RD = 2, bool XB = false, class Epi>
 __device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int ksplit, Epi& epi) {
   using S = GemmShape<WM, WN>;
   const int nm = (g.M + S::BM - 1) / S::BM, nn = N / S::BN;
   const int items = nm * nn * ksplit, kc = K / ksplit;
 #pragma unroll 1
-  for (int it = vwg(); it < items; it += NWG) {
+  for (int it = XB ? first_item(items, nm) : vwg(); it < items; it += NWG) {
     const int mt = it % nm, rest = it / nm, nt = rest % nn, sp = rest / nn;
     epi.split = sp;
     gemm_tile<WM, WN, AF, RD>(g, mt * S::BM, nt * S::BN, sp * kc, sp * kc + kc, epi);

@@ -675,7 +675,7 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
       // a three-step ring where it fits (the 128 x 64 tiles of batch 16: QKV 8.15 -> 7.32 us per layer,
       // 35.47 -> 34.95 ms per launch)
       constexpr int RD = 3 * GemmShape<WM, WN>::STEP <= RING_BYTES ? 3 : 2;
-      gemm_stage<WM, WN, AF, RD>(g, N, K, ks, e);
+      gemm_stage<WM, WN, AF, RD, true>(g, N, K, ks, e);
     }
   };
   const std::true_type frag;
@@ -721,11 +721,11 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
         gemm_stage_fixup<WM, WNG, true>(gx, GUN, D, L.ks_gu, ws, (uint32_t)L.pgu, L.MP, cnt, RING_BYTES, f);
       } else if (L.ks_gu == 1) {  // one pass of tiles covers the grid: gate fused into the epilogue
         EpiSiluGate e{ws, (uint32_t)L.h, p.b_gu + (size_t)l * GUN, 0};
-        gemm_stage<WM, WNG, true>(gx, GUN, D, 1, e);
+        gemm_stage<WM, WNG, true, 2, true>(gx, GUN, D, 1, e);
         mark(p, 10, t0);
       } else {
         EpiPartN e{{}, ws, (uint32_t)L.pgu, L.MP, GUN, 0};
-        gemm_stage<WM, WNG, true>(gx, GUN, D, L.ks_gu, e);
+        gemm_stage<WM, WNG, true, 2, true>(gx, GUN, D, L.ks_gu, e);
         sync(10);
         stage_gate(p, ws, l);
       }

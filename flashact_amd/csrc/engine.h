@@ -463,6 +463,10 @@ template <class E, class = void>
 struct HasPre : std::false_type {};
 template <class E>
 struct HasPre<E, std::void_t<typename E::Pre>> : std::true_type {};
+template <class E, class = void>
+struct IsStaged : std::false_type {};
+template <class E>
+struct IsStaged<E, std::void_t<decltype(E::kStaged)>> : std::bool_constant<E::kStaged && (E::kRowBytes > 0)> {};
 
 // Epilogue: epi(n, m, v) with features n..n+3 of token m (m < M only); an epilogue with a Pre type
 // (gemm_tile's interface) gets epi(n, m, v, pre) with every block's pre fetched before the first call.
@@ -552,6 +556,36 @@ __device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, 
       vm_wait<NA>();
     __syncthreads();
   }
+  if constexpr (!HasPre<Epi>::value && IsStaged<Epi>::value) {
+    // Staged row-out epilogue, per wave: the wave's 16 WM token rows x (128 / FW) features go through
+    // its own LDS rows (the ring is free once every wave's last MFMAs are done), then each lane
+    // stores 16 contiguous bytes of a row, so an instruction writes whole row segments (four 256-byte
+    // rows of bf16 partials) instead of 8 B into each of 16 rows.
+    constexpr int OB = Epi::kRowBytes, RB = 128 / FW / 4 * OB, RP = RB + 16, WR = 16 * WM;
+    static_assert(OB == 8 && RB % 16 == 0 && 64 % (RB / 16) == 0, "8 output bytes per 4 features");
+    __syncthreads();  // every wave's last MFMAs have read the ring
+    if (16 * tb0 < g.M) {
+      const uint32_t base = (uint32_t)w * WR * RP;
+#pragma unroll
+      for (int j = 0; j < WN; j++)
+#pragma unroll
+        for (int i = 0; i < WM; i++) {
+          const u32x4 v = epi.pack(n0 + 16 * (wf * WN + j) + 4 * lq, acc[j][i]);
+          *reinterpret_cast<u32x2*>(lds + base + (16 * i + lr) * RP + (16 * j + 4 * lq) / 4 * OB) = u32x2{v[0], v[1]};
+        }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's rows are in LDS
+      asm volatile("" ::: "memory");
+      constexpr int TPR = RB / 16, RPP = 64 / TPR;  // lanes per row, rows per instruction
+      const int tc = lane % TPR;
+#pragma unroll 4
+      for (int r = lane / TPR; r < WR; r += RPP) {
+        const int m = m0 + WR * wt + r;
+        if (m < g.M)
+          st_b128(epi.ws, epi.row_off(m, n0 + 128 / FW * wf) + (uint32_t)(tc * 16), lds128(base + (uint32_t)(r * RP + tc * 16)));
+      }
+    }
+    __syncthreads();  // the staged rows are read before the next tile's copies land
+  } else {
   if (16 * tb0 >= g.M) return;
   if constexpr (HasPre<Epi>::value) {
     typename Epi::Pre pre[WN][WM];
@@ -577,6 +611,7 @@ __device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, 
         const int m = m0 + 16 * (WM * wt + i) + lr;
         if (m < g.M) epi(n0 + 16 * (wf * WN + j) + 4 * lq, m, acc[j][i]);
       }
+  }
   }
 }
 

@@ -109,14 +109,14 @@ struct EpiGeluF {
 // 83 MB per layer at Lp = 968 (N1 and this stage's stores both bandwidth-bound). Each partial is
 // rounded once to bf16 before the fp32 sum: the precision of the reference's bf16 backbone, whose
 // residual stream itself is bf16; the range is fp32's.
-struct EpiPartB {
+struct EpiPartB {  // bf16 partial sums [split][MP][2048] of the down projection, rows staged whole
+  static constexpr int kRowBytes = 8;
+  static constexpr bool kStaged = true;
   rsrc_t ws;
   uint32_t off;
   int MP, split;
-  __device__ void operator()(int n, int m, f32x4 v) const {
-    st_b64(ws, off + (uint32_t)((((size_t)split * MP + m) * D + n) * 2),
-           u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])});
-  }
+  __device__ u32x4 pack(int, f32x4 v) const { return u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), 0u, 0u}; }
+  __device__ uint32_t row_off(int m, int n0) const { return off + (uint32_t)((((size_t)split * MP + m) * D + n0) * 2); }
 };
 
 struct EpiPart : NoPre {  // bf16 partial sums [split][MP][2048] of the O projection (as EpiPartB)
@@ -232,7 +232,9 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xi
 }
 
 constexpr uint32_t LDS_GEMM = GemmShape<4, 4>::LDS > TALL_LDS ? GemmShape<4, 4>::LDS : TALL_LDS;
-constexpr uint32_t LDS_BYTES = LDS_GEMM > ATT_LDS ? LDS_GEMM : ATT_LDS;
+constexpr uint32_t LDS_ATTG = LDS_GEMM > ATT_LDS ? LDS_GEMM : ATT_LDS;
+constexpr uint32_t LDS_STAGE = NWAVE * 64 * (256 + 16);  // the down projection's staged rows
+constexpr uint32_t LDS_BYTES = LDS_ATTG > LDS_STAGE ? LDS_ATTG : LDS_STAGE;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {

@@ -468,6 +468,12 @@ struct IsStaged : std::false_type {};
 template <class E>
 struct IsStaged<E, std::void_t<decltype(E::kStaged)>> : std::bool_constant<E::kStaged && (E::kRowBytes > 0)> {};
 
+// LDS bytes of gemm_tile_d<TW, WM>'s staged epilogue (8 output bytes per 4 features, 16 B row padding)
+template <int TW, int WM>
+constexpr uint32_t staged_d_lds() {
+  return (uint32_t)NWAVE * 16 * WM * (128 / (NWAVE / TW) / 4 * 8 + 16);
+}
+
 // Epilogue: epi(n, m, v) with features n..n+3 of token m (m < M only); an epilogue with a Pre type
 // (gemm_tile's interface) gets epi(n, m, v, pre) with every block's pre fetched before the first call.
 template <int TW, int WM, class Epi>
@@ -560,7 +566,8 @@ __device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, 
     // Staged row-out epilogue, per wave: the wave's 16 WM token rows x (128 / FW) features go through
     // its own LDS rows (the ring is free once every wave's last MFMAs are done), then each lane
     // stores 16 contiguous bytes of a row, so an instruction writes whole row segments (four 256-byte
-    // rows of bf16 partials) instead of 8 B into each of 16 rows.
+    // rows of bf16 partials) instead of 8 B into each of 16 rows. The kernel's LDS must hold
+    // staged_d_lds<TW, WM>() bytes.
     constexpr int OB = Epi::kRowBytes, RB = 128 / FW / 4 * OB, RP = RB + 16, WR = 16 * WM;
     static_assert(OB == 8 && RB % 16 == 0 && 64 % (RB / 16) == 0, "8 output bytes per 4 features");
     __syncthreads();  // every wave's last MFMAs have read the ring
@@ -573,7 +580,7 @@ __device__ __forceinline__ void gemm_tile_d(const GemmArgsF& g, int m0, int n0, 
           const u32x4 v = epi.pack(n0 + 16 * (wf * WN + j) + 4 * lq, acc[j][i]);
           *reinterpret_cast<u32x2*>(lds + base + (16 * i + lr) * RP + (16 * j + 4 * lq) / 4 * OB) = u32x2{v[0], v[1]};
         }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's rows are in LDS
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0) alone (vmcnt 63, expcnt 7): this wave's rows are in LDS
       asm volatile("" ::: "memory");
       constexpr int TPR = RB / 16, RPP = 64 / TPR;  // lanes per row, rows per instruction
       const int tc = lane % TPR;

@@ -233,7 +233,7 @@ __device__ __forceinline__ void stage_norm(const Params& p, rsrc_t ws, rsrc_t xi
 
 constexpr uint32_t LDS_GEMM = GemmShape<4, 4>::LDS > TALL_LDS ? GemmShape<4, 4>::LDS : TALL_LDS;
 constexpr uint32_t LDS_ATTG = LDS_GEMM > ATT_LDS ? LDS_GEMM : ATT_LDS;
-constexpr uint32_t LDS_STAGE = NWAVE * 64 * (256 + 16);  // the down projection's staged rows
+constexpr uint32_t LDS_STAGE = staged_d_lds<NWAVE, 4>();  // the down projection's staged rows
 constexpr uint32_t LDS_BYTES = LDS_ATTG > LDS_STAGE ? LDS_ATTG : LDS_STAGE;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 

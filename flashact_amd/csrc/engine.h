@@ -210,21 +210,25 @@ struct GemmArgs {
   int lda, ldw, M;
 };
 
-template <int WM, int WN>
+template <int WM, int WN, bool AF = false>
 struct GemmShape {
   static constexpr int BM = 32 * WM, BN = 32 * WN;
   static constexpr int GA = (BM + 63) / 64, GW = (BN + 63) / 64;  // 64-row groups
-  static constexpr int NI = 16 * (GA + GW);                       // copy instructions per step
+  // activation copies per step: 16 per 64-row group, or with AF one 1 KB fragment per 16 tokens and
+  // 32 k (BM / 4: a 96-token tile copies 24, not the 32 of two 64-row groups)
+  static constexpr int NA = AF ? BM / 4 : 16 * GA;
+  static constexpr int NI = NA + 16 * GW;                         // copy instructions per step
   static constexpr int IPW = NI / NWAVE;                          // per wave
   static constexpr uint32_t PITCH = 1040;
   static constexpr uint32_t STEP = (uint32_t)NI * PITCH;
   static constexpr uint32_t LDS = 2 * STEP;
   static_assert(BN % 64 == 0, "weight tiles are whole 64-row groups");
+  static_assert(NI % NWAVE == 0, "every wave issues the same number of copies");
 };
 
 template <int WM, int WN, bool AF = false, int RD = 2, class Epi>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int k0, int k1, Epi& epi) {
-  using S = GemmShape<WM, WN>;
+  using S = GemmShape<WM, WN, AF>;
   const int w = wave_id(), lane = lane_id(), lr = lane & 15, lq = lane >> 4;
   const int wm = w & 1, wn = (w >> 1) & 1;
   // Waves 0-3 compute (2 x 2); with 8 waves, waves 4-7 share the copies and barriers only.
@@ -234,7 +238,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
 #pragma unroll
   for (int j = 0; j < S::IPW; j++) {
     const int f = w + NWAVE * j;
-    if (f < 16 * S::GA) {
+    if (f < S::NA) {
       if constexpr (AF) {
         // blocks past the tile or past M copy the last token block of the operand (results discarded)
         int tb = (m0 >> 4) + (f >> 2);
@@ -247,7 +251,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
         src[j] = reinterpret_cast<const unsigned char*>(g.A + (size_t)row * g.lda + k0 + 8 * lr);
       }
     } else {
-      const int fw = f - 16 * S::GA;
+      const int fw = f - S::NA;
       const int row = n0 + 64 * (fw >> 4) + 16 * lq + (fw & 15);
       src[j] = reinterpret_cast<const unsigned char*>(g.W + (size_t)row * g.ldw + k0 + 8 * lr);
     }
@@ -258,7 +262,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
 #pragma unroll
     for (int j = 0; j < S::IPW; j++) {
       const int f = w + NWAVE * j;
-      if (f < 16 * S::GA)
+      if (f < S::NA)
         dma16<true>(src[j] + (AF ? 4096 : 256) * s, lds_addr(base + f * S::PITCH));
       else
         dma16<false>(src[j] + 256 * s, lds_addr(base + f * S::PITCH));
@@ -306,7 +310,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
 #pragma unroll
       for (int j = 0; j < WN; j++) {
         const int nb = wn * WN + j;
-        b[h][j] = lds128(base + (16 * (S::GA + (nb >> 2)) + lr) * S::PITCH + (nb & 3) * 256 + ks * 64 + lq * 16);
+        b[h][j] = lds128(base + (S::NA + 16 * (nb >> 2) + lr) * S::PITCH + (nb & 3) * 256 + ks * 64 + lq * 16);
       }
     };
     rd(0, 0);
@@ -419,7 +423,7 @@ __device__ __forceinline__ int first_item(int items, int gs) {
 // pi0.5 batched kernel (QKV 15.1 -> 15.5 us per layer) and the prefill (no change) keep vwg().
 template <int WM, int WN, bool AF = false, int RD = 2, bool XB = false, class Epi>
 __device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int ksplit, Epi& epi) {
-  using S = GemmShape<WM, WN>;
+  using S = GemmShape<WM, WN, AF>;
   const int nm = (g.M + S::BM - 1) / S::BM, nn = N / S::BN;
   const int items = nm * nn * ksplit, kc = K / ksplit;
 #pragma unroll 1
@@ -656,7 +660,7 @@ template <int WM, int WN, bool AF = false, class Fin>
 __device__ __forceinline__ void gemm_stage_fixup(const GemmArgs& g, int N, int K, int ksplit, rsrc_t ws,
                                                  uint32_t part_off, int MP, unsigned* counters, uint32_t flag_lds,
                                                  Fin& fin) {
-  using S = GemmShape<WM, WN>;
+  using S = GemmShape<WM, WN, AF>;
   struct Part : NoPre {
     rsrc_t ws;
     uint32_t off;

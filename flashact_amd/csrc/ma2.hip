@@ -674,7 +674,7 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
       EpiPartN e{{}, ws, part, L.MP, N, 0};
       // a three-step ring where it fits (the 128 x 64 tiles of batch 16: QKV 8.15 -> 7.32 us per layer,
       // 35.47 -> 34.95 ms per launch)
-      constexpr int RD = 3 * GemmShape<WM, WN>::STEP <= RING_BYTES ? 3 : 2;
+      constexpr int RD = 3 * GemmShape<WM, WN, AF>::STEP <= RING_BYTES ? 3 : 2;
       gemm_stage<WM, WN, AF, RD, true>(g, N, K, ks, e);
     }
   };
@@ -745,17 +745,17 @@ __global__ void __launch_bounds__(NTHR, 1) ma2_kernel(Params p) {
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Tile shapes: batches of up to 64 tokens use 32-token x 64-row tiles; larger ones 128 x 64 tiles,
-// except gate/up on 128 x 128. At batch 16 (480 tokens) the 128 x 64 tiles need no K split for QKV
-// (144 tiles) and half the splits elsewhere (down 4 instead of 8, the 768 x 768 projections 3 instead
-// of 6), so the stages that sum the partials read fewer of them. Per layer at batch 16 against
-// 128 x 128 everywhere: QKV + SATT 13.4 -> 13.1, SO + N_mca 10.6 -> 8.8, CQ 5.3 -> 4.2, CO + N_mlp
-// 10.5 -> 8.6, DN + N_msa 14.0 -> 13.9 us; 38.3 -> 36.1 ms per launch. Gate/up stays on 128 x 128
-// (16.1 us per layer on 128 x 64 against 11.0).
+// Tile shapes: batches of up to 64 tokens use 32-token x 64-row tiles; larger ones 96 x 64 tiles,
+// except gate/up on 96 x 128. At batch 16 (480 tokens = 5 x 96, no padded rows) the 96-token tiles
+// keep every stage within one pass of the 256 workgroups (QKV 180 tiles without a K split, the
+// 768 x 768 projections split 3, down 4, gate/up 240 tiles) and copy 24 activation fragments per
+// k-step where two 64-row groups took 32: 33.43 -> 31.73 ms per launch against 128-token tiles
+// (QKV 7.0 -> 5.8, gate/up 11.0 -> 9.7 us per layer), which had taken 38.3 -> 36.1 ms against 128 x 128
+// everywhere.
 constexpr int SMALL_M = 64;
 __host__ inline bool small_cfg(int M) { return M <= SMALL_M; }
 __host__ inline Layout layout_for(int B, int Tv, int Lkmax) {
-  return small_cfg(B * Tv) ? layout(B, Tv, Lkmax, 32, 64, 64) : layout(B, Tv, Lkmax, 128, 64, 128);
+  return small_cfg(B * Tv) ? layout(B, Tv, Lkmax, 32, 64, 64) : layout(B, Tv, Lkmax, 96, 64, 128);
 }
 
 }  // namespace ma2
@@ -821,7 +821,7 @@ extern "C" int fa_ma2_flow(const fa_ma2_args* a, fa_stream_t stream) {
                       need);
   if (ma2_bs1_eligible(a->batch, a->Tv, a->Lkmax)) return ma2_bs1_launch(a, stream);
   const bool sm = small_cfg(a->batch * a->Tv);
-  const void* kern = sm ? (const void*)ma2_kernel<1, 2, 2> : (const void*)ma2_kernel<4, 2, 4>;
+  const void* kern = sm ? (const void*)ma2_kernel<1, 2, 2> : (const void*)ma2_kernel<3, 2, 4>;
   int rc = host::check_device(kern, NTHR, LDS_BYTES, NWG, "fa_ma2_flow");
   if (rc != FA_OK) return rc;
   Params p;

@@ -40,9 +40,10 @@ def test_ma2_config4_bs1(gpu):
 
 # Batch 1 runs the XCD-local kernel up to Tv = 32 and Lk = 512: (1, 512, 32) fills every token lane
 # and context rank; (1, 65, 17) leaves one token in the second token tile and a ragged key chunk.
+# (1, 300, 40) runs the generic kernel's small-tile path with four waves per cross-attention item.
 @pytest.mark.parametrize("B,Lk,Tv,S,adim", [(1, 1, 1, 2, 6), (2, 700, 64, 1, 32), (3, 37, 17, 2, 5),
                                             (1, 128, 16, 1, 6), (2, 129, 33, 1, 1), (1, 512, 32, 2, 6),
-                                            (1, 65, 17, 2, 7)])
+                                            (1, 65, 17, 2, 7), (1, 300, 40, 2, 6)])
 def test_ma2_edge_shapes(gpu, B, Lk, Tv, S, adim):
     _check(C.make_case(NL=2, Lk=Lk, Tv=Tv, S=S, adim=adim, batch=B, seed=Lk + Tv), gpu)
 

@@ -279,7 +279,7 @@ __global__ void __launch_bounds__(NTHR, 1) prefill_kernel(Params p) {
     {
       EpiQKV e{ws, kc, vc, p.rope_cos, p.rope_sin, (uint32_t)L.qf, L.NQT, p.Tv, NL, p.Lmax, p.Lp, l, 0};
       gx.W = p.wqkv + (size_t)l * QKVN * D;
-      gemm_stage<4, 4>(gx, QKVN, D, 1, e);
+      gemm_stage<3, 4>(gx, QKVN, D, 1, e);  // 96-token tiles: 220 items (160 of 128): QKV 29.1 -> 26.3 us per layer
     }
     mark(p, 1, t0);
     if (l == NL - 1) break;  // the last layer's K/V are in the caches

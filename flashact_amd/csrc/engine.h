@@ -419,8 +419,9 @@ __device__ __forceinline__ int first_item(int items, int gs) {
   return it < min(ng * (x + 1) / 8 * gs, items) ? it : items;
 }
 
-// XB: items placed by first_item (batched MolmoAct2: 34.13 -> 33.34 ms per launch at batch 16); the
-// pi0.5 batched kernel (QKV 15.1 -> 15.5 us per layer) and the prefill (no change) keep vwg().
+// XB: items placed by first_item (batched MolmoAct2: 34.13 -> 33.34 ms per launch at batch 16; the
+// pi0.5 batched kernel's O and down projections, 224 items each: 19.17 -> 18.98 ms). The pi0.5 QKV
+// stage (15.1 -> 15.5 us per layer with it) and the prefill (no change) keep vwg().
 template <int WM, int WN, bool AF = false, int RD = 2, bool XB = false, class Epi>
 __device__ __forceinline__ void gemm_stage(const GemmArgs& g, int N, int K, int ksplit, Epi& epi) {
   using S = GemmShape<WM, WN, AF>;

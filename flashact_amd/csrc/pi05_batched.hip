@@ -299,7 +299,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       {
         EpiPart e{{}, ws, (uint32_t)L.part, L.MP, 0};
         ga.W = p.wo + (size_t)l * D * QD;
-        gemm_stage<4, 4, true>(ga, D, QD, KSPLIT, e);
+        gemm_stage<4, 4, true, 2, true>(ga, D, QD, KSPLIT, e);
       }
       mark(p, 4, t0);
       grid_sync(grid);
@@ -319,7 +319,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       {
         EpiPart e{{}, ws, (uint32_t)L.part, L.MP, 0};
         gh.W = p.w3 + (size_t)l * D * FF;
-        gemm_stage<4, 4, true>(gh, D, FF, KSPLIT, e);
+        gemm_stage<4, 4, true, 2, true>(gh, D, FF, KSPLIT, e);
       }
       mark(p, 7, t0);
       grid_sync(grid);

@@ -31,20 +31,46 @@ static_assert(NWAVE == 4 || NWAVE == 8, "4 or 8 waves per workgroup");
 
 extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
 
-// With 8 waves (256 registers per lane) the indices pass through an empty asm, so the compiler
-// derives each stage's addresses inside the stage instead of hoisting them out of the layer loop and
-// keeping them live across every other stage (8-wave prefill: 171 -> 20 spilled VGPRs). With 4 waves
-// the registers are there, and recomputing the addresses per stage measured slower (batch 16 19.09 ->
-// 19.42 ms).
-__device__ __forceinline__ int wave_id() {
-  int w = threadIdx.x >> 6;
-  if (NWAVE == 8) asm volatile("" : "+v"(w));
-  return __builtin_amdgcn_readfirstlane(w);
+// With 8 waves (256 registers per lane) the thread index passes through an empty asm before anything
+// is derived from it, so the compiler derives each stage's addresses inside the stage instead of
+// hoisting them out of the layer loop and keeping them live across every other stage (8-wave
+// prefill: 171 -> 20 spilled VGPRs; 0 with every thread-index use laundered, the uniform divisions
+// below and the launch sequence number in SGPRs). With 4 waves the registers are there, and
+// recomputing the addresses per stage measured slower (batch 16 19.09 -> 19.42 ms).
+__device__ __forceinline__ int tid() {
+  int t = threadIdx.x;
+  if (NWAVE == 8) asm volatile("" : "+v"(t));
+  return t;
 }
-__device__ __forceinline__ int lane_id() {
-  int l = threadIdx.x & 63;
-  if (NWAVE == 8) asm volatile("" : "+v"(l));
-  return l;
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(tid() >> 6); }
+__device__ __forceinline__ int lane_id() { return tid() & 63; }
+// Thread 0 of workgroup 0. The thread test comes from tid() behind the workgroup test, so the two
+// stay a scalar branch and a vector compare: folded into one compare, blockIdx.x gets a VGPR copy
+// that its other uses then share.
+__device__ __forceinline__ bool grid_thread0() { return blockIdx.x == 0 && tid() == 0; }
+// 1 / d for a wave-uniform d (v_rcp_f32, 1 ulp), as an SGPR value: compute it where d is known,
+// outside the loops that divide by it. The VGPR operand is laundered so that two calls do not share
+// one reciprocal kept live (or spilled) between them.
+__device__ __forceinline__ float rcp_u(int d) {
+  asm volatile("" : "+v"(d));
+  const float f = (float)d;
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, __builtin_amdgcn_rcpf(f))));
+}
+// m / d and m % d for 0 <= m < 2^20 and 0 < d, given rd = rcp_u(d): the float quotient, truncated,
+// then one correction step (the compiler's integer expansion keeps its reciprocal in a VGPR).
+struct QR {
+  int q, r;
+};
+__device__ __forceinline__ QR divmod_u(int m, int d, float rd) {
+  int q = (int)((float)m * rd), r = m - q * d;
+  if (r < 0) {
+    q -= 1;
+    r += d;
+  } else if (r >= d) {
+    q += 1;
+    r -= d;
+  }
+  return {q, r};
 }
 // XCD-major virtual workgroup index: workgroup b runs on XCD b % 8; v = xcd * 32 + rank.
 __device__ __forceinline__ int vwg() {
@@ -137,15 +163,16 @@ __device__ __forceinline__ void grid_sync(Grid& g, const F& side = F{}) {
   __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
   __syncthreads();
   g.e += 1;
-  if (threadIdx.x >= 64) side();
-  const int x = blockIdx.x & 7, rk = blockIdx.x >> 3, lane = threadIdx.x & 63;
+  const int t = tid();
+  if (t >= 64) side();
+  const int x = blockIdx.x & 7, rk = blockIdx.x >> 3, lane = t & 63;
   // flag stores through a wave-uniform descriptor (a generic pointer would keep the 64-bit address in
   // VGPRs across the whole layer loop)
   const rsrc_t r = make_rsrc(g.flags, 4096);
   const u32x2 ev = {(unsigned)g.e, (unsigned)(g.e >> 32)};
-  if (threadIdx.x == 0)  // this XCD's slot (plain store: read back from the XCD's L2 by its leader)
+  if (t == 0)  // this XCD's slot (plain store: read back from the XCD's L2 by its leader)
     stb64<kCpPlain>(r, (uint32_t)(x * 32 + rk) * 8, ev);
-  if (threadIdx.x < 64 && !(__hip_atomic_load(g.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin)) {
+  if (t < 64 && !(__hip_atomic_load(g.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSpin)) {
     auto wait = [&](bool mine, uint32_t off) {
       for (unsigned it = 0;; ++it) {
         const u32x2 v = ldb64<kCpSc1>(r, mine ? off : 0x80000000u);
@@ -351,9 +378,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int m0, int n0, int
       }
     __syncthreads();
     constexpr int TPR = RB / 16, RPP = NTHR / TPR;  // threads per row, rows per pass
-    const int tc = threadIdx.x % TPR;
+    const int t = tid(), tc = t % TPR;
 #pragma unroll 4
-    for (int r = threadIdx.x / TPR; r < S::BM; r += RPP) {
+    for (int r = t / TPR; r < S::BM; r += RPP) {
       const int m = m0 + r;
       if (m < g.M) st_b128(epi.ws, epi.row_off(m, n0) + (uint32_t)(tc * 16), lds128((uint32_t)(r * RP + tc * 16)));
     }
@@ -706,7 +733,7 @@ __device__ __forceinline__ void gemm_stage_fixup(const GemmArgs& g, int N, int K
     __syncthreads();
     if (!*flag) continue;
 #pragma unroll 1
-    for (int e = threadIdx.x; e < S::BM * Q; e += NTHR) {
+    for (int e = tid(); e < S::BM * Q; e += NTHR) {
       const int m = mt * S::BM + e / Q, n = nt * S::BN + 4 * (e % Q);
       if (m >= g.M) continue;
       u32x4 v[FIXUP_MAX_KS];

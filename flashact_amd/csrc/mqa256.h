@@ -37,16 +37,18 @@ struct EpiQKV {
   const float* rsin;
   uint32_t qf;
   int NQT, Tv, NL, Lmax, Lp, l, split;
+  float rtv;  // rcp_u(Tv)
   typedef f32x4 Pre;  // cos j0, cos j0+1, sin j0, sin j0+1 of the lane's token
   __device__ Pre pre(int n0, int m) const {
     if (n0 >= 2304) return f32x4{0.f, 0.f, 0.f, 0.f};
-    const int t = m % Tv, j0 = ((n0 < 2048 ? n0 : n0 - 2048) >> 1) & 127;
+    const int t = divmod_u(m, Tv, rtv).r, j0 = ((n0 < 2048 ? n0 : n0 - 2048) >> 1) & 127;
     const f32x2 c = *reinterpret_cast<const f32x2*>(rcos + t * 128 + j0);
     const f32x2 sn = *reinterpret_cast<const f32x2*>(rsin + t * 128 + j0);
     return f32x4{c[0], c[1], sn[0], sn[1]};
   }
   __device__ void operator()(int n0, int m, f32x4 v, f32x4 cs) const {
-    const int b = m / Tv, t = m - b * Tv;
+    const QR bt = divmod_u(m, Tv, rtv);
+    const int b = bt.q, t = bt.r;
     if (n0 >= 2304) {  // v rows: dims n0-2304 .. +3 of key Lp+t
       const int d0 = n0 - 2304;
       const size_t base = (((size_t)b * NL + l) * HD + d0) * Lmax + Lp + t;
@@ -220,8 +222,9 @@ __device__ __forceinline__ void stage_att(const P& p, rsrc_t ws, int l) {
           // Keys [kend, ...) of the 8-key group that straddles kend come from cache rows past
           // Ltot: zero them in V^T so that P = 0 meets a finite value. (Groups wholly past Ltot
           // were copied from key 0 instead.) One thread per dim: the first 256 threads.
-          if (threadIdx.x < HD) {
-            const int d = threadIdx.x, gk = (kend - key0) >> 3, nv = (kend - key0) & 7;
+          const int d = tid();
+          if (d < HD) {
+            const int gk = (kend - key0) >> 3, nv = (kend - key0) & 7;
             const uint32_t off = ATT_VB + (d & 63) * ATT_PITCH + (d >> 6) * 256 + gk * 16;
             u32x4 v = lds128(off);
 #pragma unroll
@@ -293,6 +296,7 @@ __device__ __forceinline__ void stage_comb(const P& p, rsrc_t ws) {
   const int dp = l16 >> 1, jh = l16 & 1;  // lane: dims 32 dp + 8 jh .. + 7 and 32 dp + 16 + 8 jh .. + 7
   const int Ltot = p.Lp + p.Tv, nkc = (Ltot + KCH - 1) / KCH;
   const int rows = p.B * NH * p.Tv;
+  const float rnt = rcp_u(NH * p.Tv), rtv = rcp_u(p.Tv);
   // with 8 waves, wave-major (consecutive rows on different CUs first), so rows spread over every CU
   const int slot = NWAVE == 8 ? wave_id() * NWG + vwg() : vwg() * NWAVE + wave_id();
 #pragma unroll 1
@@ -300,7 +304,8 @@ __device__ __forceinline__ void stage_comb(const P& p, rsrc_t ws) {
     const int R = R0 + sub;
     const bool valid = R < rows;
     const int Rc = valid ? R : R0;
-    const int b = Rc / (NH * p.Tv), r = Rc - b * NH * p.Tv, h = r / p.Tv, t = r - h * p.Tv;
+    const QR br = divmod_u(Rc, NH * p.Tv, rnt), ht = divmod_u(br.r, p.Tv, rtv);
+    const int b = br.q, r = br.r, h = ht.q, t = ht.r;
     const size_t cstride = (size_t)L.NQT * 16;  // rows per chunk
     const size_t row0 = (size_t)b * L.NKC * cstride + r;
     const size_t tile0 = (size_t)b * L.NKC * L.NQT + (r >> 4);

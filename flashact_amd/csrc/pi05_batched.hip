@@ -259,6 +259,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
     __hip_atomic_store(reinterpret_cast<unsigned*>(p.ws + kWsOwner), kOwnerPi05Batched, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   const int NL = p.NL;
+  const float rtv = rcp_u(p.Tv);
   const float dt = -1.0f / (float)p.S;
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   const uint32_t mb16 = (uint32_t)((L.M + 15) / 16 * 16);  // tokens of the fragment-ordered operands
@@ -281,7 +282,7 @@ __global__ void __launch_bounds__(NTHR, 1) pi05_batched_kernel(Params p) {
       grid_sync(grid);
       mark(p, 9, t0);
       {
-        EpiQKV e{ws, kc, vc, p.rope_cos, p.rope_sin, (uint32_t)L.qf, L.NQT, p.Tv, NL, p.Lmax, p.Lp, l, 0};
+        EpiQKV e{ws, kc, vc, p.rope_cos, p.rope_sin, (uint32_t)L.qf, L.NQT, p.Tv, NL, p.Lmax, p.Lp, l, 0, rtv};
         gx.W = p.w1 + (size_t)l * 2560 * D;
         gemm_stage<3, 4, true>(gx, 2560, D, 1, e);  // 96-token tiles: 180 items fill more of the 256 CUs than 140
       }

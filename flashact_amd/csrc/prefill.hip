@@ -238,9 +238,9 @@ constexpr uint32_t LDS_BYTES = LDS_ATTG > LDS_STAGE ? LDS_ATTG : LDS_STAGE;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ void mark(const Params& p, int idx, uint64_t& t0) {
-  if (p.stage_cycles && blockIdx.x == 0 && threadIdx.x == 0) {
+  if (p.stage_cycles) {  // t0 moves in every wave: a value set under the thread test would live in VGPRs
     const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
-    p.stage_cycles[idx] += t1 - t0;
+    if (grid_thread0()) p.stage_cycles[idx] += t1 - t0;
     t0 = t1;
   }
 }
@@ -254,13 +254,17 @@ __global__ void __launch_bounds__(NTHR, 1) prefill_kernel(Params p) {
   Grid grid;
   grid.flags = reinterpret_cast<uint64_t*>(p.ws + OFF_FLAGS);
   grid.err = reinterpret_cast<unsigned*>(p.ws + OFF_CTRL + 8);
-  const uint64_t seq = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
+  // every lane loaded the same word: its halves go to SGPRs, and so do the barrier epochs after it
+  const uint64_t seq_v = ld_flag(reinterpret_cast<const uint64_t*>(p.ws + OFF_CTRL));
+  const uint64_t seq = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(seq_v >> 32)) << 32 |
+                       (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)seq_v);
   grid.e = seq << 32;
-  if (threadIdx.x == 0 && xcc_id() != (blockIdx.x & 7u)) atomicOr(grid.err, kErrXcd);
-  if (blockIdx.x == 0 && threadIdx.x == 0)
+  if (xcc_id() != (blockIdx.x & 7u) && tid() == 0) atomicOr(grid.err, kErrXcd);
+  if (grid_thread0())
     __hip_atomic_store(reinterpret_cast<unsigned*>(p.ws + kWsOwner), kOwnerPrefill, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   const int NL = p.NL;
+  const float rtv = rcp_u(p.Tv);
   uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   const uint32_t mb16 = (uint32_t)((L.M + 15) / 16 * 16);  // tokens of the fragment-ordered operands
   GemmArgsF gxf{make_rsrc(p.ws + L.xn, mb16 * D * 2), nullptr, D / 32, D, L.M};
@@ -277,7 +281,7 @@ __global__ void __launch_bounds__(NTHR, 1) prefill_kernel(Params p) {
     grid_sync(grid);
     mark(p, 9, t0);
     {
-      EpiQKV e{ws, kc, vc, p.rope_cos, p.rope_sin, (uint32_t)L.qf, L.NQT, p.Tv, NL, p.Lmax, p.Lp, l, 0};
+      EpiQKV e{ws, kc, vc, p.rope_cos, p.rope_sin, (uint32_t)L.qf, L.NQT, p.Tv, NL, p.Lmax, p.Lp, l, 0, rtv};
       gx.W = p.wqkv + (size_t)l * QKVN * D;
       gemm_stage<3, 4>(gx, QKVN, D, 1, e);  // 96-token tiles: 220 items (160 of 128): QKV 29.1 -> 26.3 us per layer
     }
@@ -322,7 +326,7 @@ __global__ void __launch_bounds__(NTHR, 1) prefill_kernel(Params p) {
     grid_sync(grid);
     mark(p, 9, t0);
   }
-  if (blockIdx.x == 0 && threadIdx.x == 0)
+  if (grid_thread0())
     __hip_atomic_store(reinterpret_cast<uint64_t*>(p.ws + OFF_CTRL), seq + 1, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -36,7 +36,7 @@ MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 # L2 <-> memory bytes of one pi05_denoise_bs1 launch at this workload, from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE passes scaled by a 1 GiB device copy (TRAFFIC_SOURCE). Counters cannot be read inside a
 # timed run, so the figure is the last measured one for this kernel, labelled as such in the JSON.
-TRAFFIC_BYTES = {"fetch": 13_209_378_215, "write": 2_113_651_220}
+TRAFFIC_BYTES = {"fetch": 13_208_372_720, "write": 2_113_680_420}
 TRAFFIC_SOURCE = ("profiles/pi05_denoise_bs1_traffic.md: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over "
                   "bench.py, scaled by a 1 GiB copy; measured in a separate profiling run, not in this one")
 

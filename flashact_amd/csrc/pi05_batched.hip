@@ -31,6 +31,7 @@ using namespace fa::mqa;
 constexpr int D = 1024, AD = 32, FF = 4096;
 constexpr int KSPLIT = 4;    // K split of the O and down projections
 constexpr int MAX_TOKENS = 4096;
+static_assert((size_t)NH * MAX_TOKENS < (1u << 20), "divmod_u: the combine rows stay below 2^20");
 
 // Workspace layout (bytes), a function of (B, Tv, Lmax).
 struct Layout {

@@ -36,6 +36,7 @@ constexpr int D = 2048, FF = 16384;
 constexpr int QKVN = QD + 2 * HD;  // 2560 projection rows
 constexpr int KS_O = 2, KS_DN = 8;  // K splits of the O and down projections
 constexpr int MAX_TOKENS = 16384;  // batch x Lp
+static_assert((size_t)NH * MAX_TOKENS < (1u << 20), "divmod_u: the combine rows stay below 2^20");
 
 struct Layout {
   int B, Tv, M, MP, NQT, NKC;
